@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X batch-shared block-sparse GEMM (one JSON line on stdout).
+
+Workload: Llama-2-7B down_proj, B=16, K=11008 (172 blocks of 64),
+N=4096, fp16, sweeping block sparsity {0, 0.25, 0.5, 0.638, 0.8}; the 0% point runs the same
+kernel with every block active (the in-run dense baseline).  One "step" = every sweep point
+once, where a point is a hipGraph of R back-to-back GEMM launches, each on a different copy
+of the packed weight (R copies span >= 1 GiB, so the 256 MB Infinity Cache cannot serve a
+repeat and the bytes really come from HBM).
+
+value  = active-weight bytes of all GEMMs in the timed steps / timed seconds (GB/s)
+roofline = the s=0.5 sparse GEMM (86/172 blocks): algorithmic bytes na*64*N*2 per launch over
+           the average launch duration from HIP events around its graph replays.
+cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul) on the s=0.5 point.
+
+    python bench.py [--steps K] [--warmup W] [--workload down_sweep|llama|fused]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(ROOT, "towards-batched-activation-sparsity_amd")
+for _p in (PKG_ROOT, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 1 << 30
+METRIC = "µs/GEMM + HBM GB/s + speedup vs dense, Llama-2-7B shapes at B=2/16/64"
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_down_b16_s050.json")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="down_sweep", choices=["down_sweep", "llama", "fused"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+class Point:
+    """One GEMM configuration: packed weight copies + a graph of R rotated launches."""
+
+    def __init__(self, name, bt, k, n, na, x_dist, seed, dev, dense=False, plan=None):
+        import numpy as np
+        import torch
+
+        import bsa_mi355x as bsa
+        from oracle import bsg_oracle as orc
+
+        self.name, self.bt, self.k, self.n, self.na, self.dense = name, bt, k, n, na, dense
+        nb = orc.nblk_of(k)
+        self.nblk = nb
+        x, w_kn, idx = orc.make_inputs(seed, bt, k, n, x_dist, na=(nb if dense else na))
+        self.x_np, self.w_kn_np, self.idx_np = x, w_kn, idx
+        self.x = torch.from_numpy(x).to(dev)
+        w_kn_t = torch.from_numpy(w_kn).to(dev)
+        packed = bsa.pack_weight(w_kn_t, layout="kn")
+        del w_kn_t
+        self.copies = max(1, math.ceil(ROTATE_BYTES / packed.numel() / 2))
+        self.packed = [packed] + [packed.clone() for _ in range(self.copies - 1)]
+        self.idx = torch.from_numpy(idx).to(dev)
+        self.y = torch.empty(bt, n, dtype=torch.float16, device=dev)
+        self.plan = bsa.resolve_plan(bt, n, nb, nb if dense else na, dev, plan)
+        self.active_bytes = (nb if dense else na) * 64 * n * 2
+        self.flops = 2 * bt * (nb if dense else na) * 64 * n
+        self.graph = None
+
+    def launch(self, i):
+        import bsa_mi355x as bsa
+
+        p = self.packed[i % self.copies]
+        if self.dense:
+            bsa.gemm_packed(self.x, p, self.n, None, self.y, plan=self.plan, workspace_prefix=f"bench_{self.name}")
+        else:
+            bsa.gemm_packed(self.x, p, self.n, self.idx, self.y, plan=self.plan, workspace_prefix=f"bench_{self.name}")
+
+    def capture(self):
+        import torch
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(self.copies):
+                self.launch(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(self.copies):
+                self.launch(i)
+        torch.cuda.synchronize()
+        self.graph = g
+
+    def check(self):
+        """Parity of the benchmarked launch against the oracle (fp32 CPU path)."""
+        import numpy as np
+        import torch
+
+        from oracle import bsg_oracle as orc
+
+        self.launch(0)
+        torch.cuda.synchronize()
+        w_nk = np.ascontiguousarray(self.w_kn_np.T)
+        ref = orc.gemm_ref(self.x_np, w_nk, self.idx_np)
+        y = self.y.float().cpu().numpy()
+        return orc.rel_frobenius(y, ref), orc.within_tolerance(y, ref)
+
+
+def time_points(points, steps, warmup):
+    """Warm-up, then exactly `steps` steps (each point's graph replayed once per step), with a
+    per-point HIP-event pair on the launch stream around every replay."""
+    import torch
+
+    for _ in range(warmup):
+        for p in points:
+            p.graph.replay()
+    torch.cuda.synchronize()
+    ev = {p.name: [] for p in points}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start_all = torch.cuda.Event(enable_timing=True)
+    end_all = torch.cuda.Event(enable_timing=True)
+    start_all.record()
+    for _ in range(steps):
+        for p in points:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            p.graph.replay()
+            b.record()
+            ev[p.name].append((a, b))
+    end_all.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start_all.elapsed_time(end_all)
+    per = {}
+    for p in points:
+        us = [a.elapsed_time(b) * 1000.0 / p.copies for a, b in ev[p.name]]
+        per[p.name] = (statistics.median(us), statistics.mean(us))
+    return total_ms, wall, per
+
+
+def cpu_baseline(point, seconds):
+    import torch
+
+    from oracle import bsg_oracle as orc
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    x = torch.from_numpy(point.x_np)
+    w = torch.from_numpy(point.w_kn_np)
+    idx = torch.from_numpy(point.idx_np.astype("int64"))
+    for _ in range(2):
+        orc.gemm_ref_torch(x, w, idx)
+    samples = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(samples) < 500:
+        t = time.perf_counter_ns()
+        orc.gemm_ref_torch(x, w, idx)
+        samples.append((time.perf_counter_ns() - t) / 1e3)
+    us = statistics.median(samples)
+    return {
+        "value": round(point.active_bytes / (us * 1e-6) / 1e9, 2),
+        "unit": "GB/s",
+        "us_per_gemm": round(us, 1),
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle gemm_ref_torch (torch CPU gather + fp32 matmul) on {point.name}: B={point.bt} "
+                   f"K={point.k} N={point.n} {point.na}/{point.nblk} blocks; {len(samples)} timed runs after 2 "
+                   f"warm-ups, median"),
+    }
+
+
+def load_traffic():
+    try:
+        with open(PROFILE_TRAFFIC) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import bsa_mi355x as bsa
+    from oracle import bsg_oracle as orc
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bsa.load()
+    log(f"device {torch.cuda.get_device_name(dev)}; lib {bsa.load().bsg_version().decode()}")
+
+    if args.workload == "down_sweep":
+        k, n, bt = 11008, 4096, 16
+        points = []
+        for s in (0.0, 0.25, 0.5, 0.638, 0.8):
+            na = orc.n_active_for_sparsity(s, orc.nblk_of(k))
+            name = "down_b16_dense" if s == 0.0 else f"down_b16_s{int(round(s * 1000)):03d}"
+            points.append(Point(name, bt, k, n, na, "laplace", 1234, dev, dense=(s == 0.0)))
+            log(f"prepared {name}: na={na} copies={points[-1].copies} plan={points[-1].plan}")
+        workload = "down_proj B=16 K=11008 N=4096 fp16, block sparsity sweep {0,0.25,0.5,0.638,0.8} (configs[1])"
+        focus = "down_b16_s500"
+    elif args.workload == "llama":
+        shapes = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
+        points = []
+        for bt, s in ((2, 0.803), (16, 0.638), (64, 0.520)):
+            for sh, (k, n) in shapes.items():
+                na = orc.n_active_for_sparsity(s, orc.nblk_of(k))
+                name = f"{sh}_b{bt}_s{int(round(s * 1000)):03d}"
+                points.append(Point(name, bt, k, n, na, "laplace" if sh == "down" else "normal", 1234, dev))
+                points.append(Point(f"{sh}_b{bt}_dense", bt, k, n, na, "laplace" if sh == "down" else "normal", 1234,
+                                    dev, dense=True))
+                log(f"prepared {name}: na={na} plan={points[-2].plan}")
+        workload = "Llama-2-7B q/k/v/o, gate/up, down at B=2@0.803, B=16@0.638, B=64@0.520 (configs[2])"
+        focus = "gate_up_b64_s520"
+    else:
+        raise SystemExit("workload 'fused' is measured by tests and DESIGN notes; not a bench line yet")
+
+    bad = []
+    for p in points:
+        rf, ok = p.check()
+        if not ok:
+            bad.append((p.name, rf))
+    if bad:
+        raise SystemExit(f"parity failure before timing: {bad}")
+    log("parity ok on every point")
+    for p in points:
+        p.capture()
+    log("graphs captured")
+
+    total_ms, wall, per = time_points(points, args.steps, args.warmup)
+    step_bytes = sum(p.active_bytes * p.copies for p in points)
+    value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
+    log(f"timed {args.steps} steps in {total_ms:.2f} ms (host wall {wall * 1e3:.1f} ms)")
+
+    dense_us = {}
+    for p in points:
+        if p.dense:
+            dense_us[p.name.replace("_dense", "")] = per[p.name][0]
+    out_points = []
+    for p in points:
+        med, mean = per[p.name]
+        gbs = p.active_bytes / (med * 1e-6) / 1e9
+        row = {"name": p.name, "B": p.bt, "K": p.k, "N": p.n, "active_blocks": p.nblk if p.dense else p.na,
+               "nblk": p.nblk, "us_per_gemm": round(med, 3), "GBps_active": round(gbs, 1),
+               "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+               "plan": list(p.plan.as_tuple())}
+        if p.bt >= 16:
+            row["mfma_util"] = round(p.flops / (med * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 5)
+        if not p.dense:
+            key = p.name.rsplit("_s", 1)[0] if args.workload == "llama" else "down_b16"
+            d = dense_us.get(key)
+            if d:
+                row["speedup_vs_dense"] = round(d / med, 3)
+                row["ideal_speedup"] = round(p.nblk / p.na, 3)
+                row["speedup_over_ideal"] = round((d / med) / (p.nblk / p.na), 3)
+        out_points.append(row)
+        log(json.dumps(row))
+
+    fp = next(p for p in points if p.name == focus)
+    f_med, f_mean = per[focus]
+    achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                "kernel": "bsg_gemm_kernel", "point": focus, "avg_launch_us": round(f_mean, 3),
+                "bytes_per_launch": fp.active_bytes}
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(fp, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) stored [K,N], X~Laplace(0,0.05)/N(0,1), "
+                "masks rng.choice sorted; weights rotated over >=1 GiB of copies",
+        "config": {"workload": workload, "gemms_per_step": sum(p.copies for p in points),
+                   "value_is": "active-weight bytes / timed seconds over all sweep points"},
+        "points": out_points,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

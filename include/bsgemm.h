@@ -1,0 +1,159 @@
+/*
+ * bsgemm.h — C ABI of the MI355X (gfx950) batch-shared 64-channel block-sparse GEMM.
+ *
+ *   Y[bt, N] = sum over active K-blocks j of  X[bt, 64j:64j+64] · W[64j:64j+64, N]
+ *
+ * One block mask (a list of active 64-channel K-blocks) is shared by every row of the
+ * decode batch.  Inputs and output are fp16 or bf16, accumulation is fp32, indices int32.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers; `stream` is a hipStream_t passed as void* (0 = null stream).
+ *   - Nothing here allocates device memory or synchronises the host: every call only enqueues
+ *     kernels on `stream`, so every call is safe inside hipStreamBeginCapture/EndCapture.
+ *   - Return value: BSG_OK (0) or a negative BSG_ERR_* code; bsg_last_error() gives a
+ *     thread-local message for the last failing call on the calling thread.
+ *   - Argument validation happens on the host before any HIP call, so an invalid call
+ *     never launches a kernel.
+ *
+ * Packed weight layout ("tiled K-major"): for K-block j (64 rows of K), column tile t
+ * (16 columns of N), k-half h, 8-row group g, column c, row e (k = 32h + 8g + e,
+ * n = 16t + c) the element lives at
+ *     j*64*Np + t*1024 + h*512 + g*128 + c*8 + e            (Np = N rounded up to 16)
+ * so each K-block is one contiguous 128*Np-byte slab and each 16-column tile of it is a
+ * contiguous 2 KiB run that one 64-lane dwordx4 load per k-half brings straight into
+ * the A operand of v_mfma_f32_16x16x32_{f16,bf16}.  Rows k >= K and columns n >= N are 0.
+ */
+#ifndef BSGEMM_H
+#define BSGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BSG_BLOCK_K 64           /* channels per K-block (reference INDEX_BLOCK_META_SIZE) */
+#define BSG_MAX_NBLK 2048        /* K <= 131072 */
+
+enum bsg_dtype { BSG_F16 = 0, BSG_BF16 = 1 };
+
+enum bsg_status {
+  BSG_OK = 0,
+  BSG_ERR_ARG = -1,         /* bad size, null pointer, inconsistent arguments */
+  BSG_ERR_DTYPE = -2,       /* dtype not fp16/bf16 */
+  BSG_ERR_WORKSPACE = -3,   /* workspace missing or smaller than *_workspace_bytes() */
+  BSG_ERR_ALIGN = -4,       /* pointer or leading dimension not 16-byte aligned */
+  BSG_ERR_UNSUPPORTED = -5, /* plan or shape outside what the kernels implement */
+  BSG_ERR_HIP = -100        /* a HIP runtime call failed; see bsg_last_error() */
+};
+
+/* Launch plan of the GEMM.  A zero field means "choose automatically".
+ *   split_k         : work-groups that share one output tile and split the active-block
+ *                     list (fp32 partials + in-kernel deterministic reduction), >= 1
+ *   cols_per_wave   : output columns per wavefront and per work-group: 16, 32, 64 or 128
+ *   waves_per_group : wavefronts per work-group; they split the block list and reduce
+ *                     through LDS: 1, 2, 4 or 8
+ *   depth           : K-blocks whose loads each wave keeps in flight: 1, 2, 4 or 8
+ *   rows_per_group  : batch rows per work-group (16, 32 or 64); bt above it adds grid rows
+ * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
+ * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
+typedef struct bsg_plan {
+  int32_t split_k;
+  int32_t cols_per_wave;
+  int32_t waves_per_group;
+  int32_t depth;
+  int32_t rows_per_group;
+} bsg_plan;
+
+/* Library identification and thread-local error message. */
+const char* bsg_version(void);
+const char* bsg_last_error(void);
+
+/* Bytes of the packed weight for a logical W[N,K]. */
+int64_t bsg_packed_bytes(int64_t N, int64_t K, int dtype);
+
+/* Pack W into the tiled K-major layout.  W is addressed as W[n][k] = w[n*stride_n + k*stride_k]
+ * (nn.Linear [N,K]: stride_n=K, stride_k=1; a [K,N] matrix: stride_n=1, stride_k=N).
+ * Replaces _get_prepacked_weight_block_major
+ * (kernels/shared_mask_batched_triton_min_runtime.py:3133-3163), which builds
+ * pad(W^T).view(nblk, 64, N); the cache around it stays in the host layer. */
+int bsg_pack_weight(const void* w, int64_t N, int64_t K, int64_t stride_n, int64_t stride_k,
+                    int dtype, void* wp, int64_t wp_bytes, void* stream);
+
+/* Resolve a plan: fills every zero field of *plan for this problem (bt rows, N columns,
+ * nblk = ceil(K/64) blocks, na active blocks) on a device with cu_count compute units.
+ * Validates non-zero fields.  Host-only; no HIP call. */
+int bsg_plan_resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu_count,
+                     bsg_plan* plan);
+
+/* Workspace bytes the GEMM needs for this resolved plan (0 when split_k == 1).
+ * The workspace holds fp32 partials and per-tile arrival counters; the counter region
+ * must be zero before first use (bsg_workspace_init) and every GEMM leaves it zero. */
+int64_t bsg_gemm_workspace_bytes(int64_t bt, int64_t N, const bsg_plan* plan);
+int bsg_workspace_init(void* ws, int64_t ws_bytes, void* stream);
+
+/* Block-sparse GEMM from an active-block index list.
+ *   x            : [bt, K] activations, row stride ldx (elements); K % 8 == 0, ldx % 8 == 0,
+ *                  16-byte aligned base
+ *   wp           : packed weight from bsg_pack_weight(N, K)
+ *   active_blocks: int32 list of K-block ids, length num_active (host count) — or, when
+ *                  num_active_dev != NULL, length *num_active_dev read on the device
+ *                  (capacity num_active, which bounds the device count)
+ *                  ids outside [0, ceil(K/64)) contribute nothing
+ *   y            : [bt, N] output, row stride ldy (elements); written, never read
+ * num_active == 0 (host count) writes zeros, like the reference's out.zero_().
+ * Replaces, with one kernel family:
+ *   _prepacked_block_sparse_gemm_from_active_blocks      (…min_runtime.py:3166-3344)
+ *   _prepacked_block_sparse_gemm_from_active_blocks_splitk (…min_runtime.py:1350-1454)
+ *   prepacked_block_sparse_gemm_batched_kernel / _splitk_write_kernel / _splitk_reduce_kernel
+ *                                                          (…min_runtime.py:684-733, 1898-1988) */
+int bsg_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K,
+             const void* wp, int64_t N,
+             const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev,
+             void* y, int64_t ldy, int dtype,
+             void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
+/* Same GEMM driven by a u8 bitmap[total_k_blocks] (non-zero = active; 1 <= total_k_blocks <=
+ * ceil(K/64), later blocks count as inactive), compacted on the
+ * device into ascending block order; the block list never leaves the GPU.
+ * Replaces _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload(_splitk) and
+ * prepacked_block_sparse_gemm_bitmap_preload_batched_kernel / _splitk_kernel
+ * (…min_runtime.py:814-874, 1064-1147, 1150-1216, 1235-1347). */
+int bsg_gemm_bitmap(const void* x, int64_t ldx, int64_t bt, int64_t K,
+                    const void* wp, int64_t N,
+                    const uint8_t* bitmap, int32_t total_k_blocks,
+                    void* y, int64_t ldy, int dtype,
+                    void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
+/* The same kernel with every K-block active: the in-run dense baseline.  Stands in for the
+ * reference's dense torch.mm(x, W^T) (scripts/bench_perstep_actual_kernel_speedup.py:162,
+ * scripts/profile_kernel_configs.py:229). */
+int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K,
+                   const void* wp, int64_t N,
+                   void* y, int64_t ldy, int dtype,
+                   void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
+/* Fused online block selector: score_j = sum_b sum_{c in block j} |x[b, 64j+c]| computed
+ * exactly (integer units of 2^-24), top-k by (score desc, block id asc), compacted to an
+ * ascending int32 list idx_out[min(k, nblk)] with the count written to *na_out (device).
+ * One launch; the mask never round-trips to the host.  Replaces the torch op chain of
+ * _select_active_blocks (scripts/bench_roundrobin_e2e_decode.py:90-113) with the L1 rule. */
+int64_t bsg_select_workspace_bytes(int64_t K);
+int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k,
+                       int32_t* idx_out, int32_t* na_out, int dtype,
+                       void* ws, int64_t ws_bytes, void* stream);
+
+/* Selector followed by the GEMM on its device-side list, both on `stream`.
+ * ws is split: the first bsg_select_workspace_bytes(K) bytes for the selector, the rest
+ * (bsg_gemm_workspace_bytes) for the GEMM.  Replaces the select -> bitmap -> GEMM sequence
+ * of _sparse_linear (scripts/bench_roundrobin_e2e_decode.py:179-284). */
+int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k,
+                    const void* wp, int64_t N, int32_t* idx_out, int32_t* na_out,
+                    void* y, int64_t ldy, int dtype,
+                    void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BSGEMM_H */

@@ -1,0 +1,148 @@
+"""The C-ABI library (no GPU needed): it loads, exports every symbol include/bsgemm.h declares,
+and rejects invalid arguments on the host before any HIP call."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+import bsa_mi355x as bsa
+from bsa_mi355x import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bsgemm.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bsg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_and_library_exports_everything():
+    lib = bsa.load()
+    names = _declared()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version():
+    assert b"gfx950" in bsa.load().bsg_version()
+
+
+def test_packed_bytes():
+    lib = bsa.load()
+    assert lib.bsg_packed_bytes(4096, 11008, 0) == 172 * 64 * 4096 * 2
+    assert lib.bsg_packed_bytes(100, 1000, 0) == 16 * 64 * 112 * 2
+    assert lib.bsg_packed_bytes(0, 64, 0) == -1
+    assert lib.bsg_packed_bytes(16, 64, 7) == -1
+
+
+def _resolve(bt, n, nblk, na, cu=256, plan=None):
+    p = plan or _lib.Plan()
+    rc = bsa.load().bsg_plan_resolve(bt, n, nblk, na, cu, ctypes.byref(p))
+    return rc, p
+
+
+def test_plan_resolve_auto_fills_every_field():
+    rc, p = _resolve(16, 4096, 172, 86)
+    assert rc == 0
+    assert p.split_k >= 1 and p.cols_per_wave in (16, 32, 64, 128) and p.waves_per_group in (1, 2, 4, 8)
+    assert p.depth in (1, 2, 4, 8) and p.rows_per_group == 16
+    assert _resolve(64, 4096, 64, 31)[1].rows_per_group == 64
+    assert _resolve(2, 4096, 64, 0)[1].split_k == 1
+
+
+def test_plan_resolve_rejects():
+    assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(300, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert "plan" in _lib.last_error()
+
+
+def test_workspace_bytes():
+    lib = bsa.load()
+    p = _lib.Plan(1, 32, 4, 4, 16)
+    assert lib.bsg_gemm_workspace_bytes(16, 4096, ctypes.byref(p)) == 0
+    p = _lib.Plan(4, 32, 4, 4, 16)
+    tiles = 4096 // 32
+    assert lib.bsg_gemm_workspace_bytes(16, 4096, ctypes.byref(p)) == 512 + tiles * 4 * 2 * 64 * 16
+    assert lib.bsg_select_workspace_bytes(4096) == 768
+    assert lib.bsg_select_workspace_bytes(0) == -1
+
+
+FAKE = 1 << 40  # never dereferenced: every call below fails validation first
+
+
+def test_gemm_rejects_bad_arguments_without_launching():
+    lib = bsa.load()
+    p = _lib.Plan(2, 32, 4, 4, 16)
+    ok = dict(x=FAKE, ldx=4096, bt=16, K=4096, wp=FAKE, N=4096, idx=FAKE, na=10, nad=None, y=FAKE, ldy=4096,
+              dtype=0, ws=FAKE, ws_bytes=1 << 30)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.bsg_gemm(a["x"], a["ldx"], a["bt"], a["K"], a["wp"], a["N"], a["idx"], a["na"], a["nad"], a["y"],
+                            a["ldy"], a["dtype"], a["ws"], a["ws_bytes"], ctypes.byref(p), None)
+
+    assert call(dtype=3) == _lib.BSG_ERR_DTYPE
+    assert call(x=None) == _lib.BSG_ERR_ARG
+    assert call(K=100) == _lib.BSG_ERR_ALIGN
+    assert call(ldx=4100) == _lib.BSG_ERR_ALIGN
+    assert call(x=FAKE + 8) == _lib.BSG_ERR_ALIGN
+    assert call(ldy=100) == _lib.BSG_ERR_ARG
+    assert call(na=-1) == _lib.BSG_ERR_ARG
+    assert call(na=5000) == _lib.BSG_ERR_ARG
+    assert call(idx=None) == _lib.BSG_ERR_ARG
+    assert call(ws=None) == _lib.BSG_ERR_WORKSPACE
+    assert call(ws_bytes=16) == _lib.BSG_ERR_WORKSPACE
+    assert call(K=200000) == _lib.BSG_ERR_UNSUPPORTED
+    assert "workspace" in _lib.last_error() or "K" in _lib.last_error()
+
+
+def test_bitmap_and_select_reject_bad_arguments():
+    lib = bsa.load()
+    p = _lib.Plan(1, 32, 4, 4, 16)
+    assert lib.bsg_gemm_bitmap(FAKE, 4096, 16, 4096, FAKE, 4096, None, 64, FAKE, 4096, 0, None, 0,
+                               ctypes.byref(p), None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_gemm_bitmap(FAKE, 4096, 16, 4096, FAKE, 4096, FAKE, 65, FAKE, 4096, 0, None, 0,
+                               ctypes.byref(p), None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_select_topk_l1(FAKE, 4096, 16, 4096, 8, FAKE, FAKE, 1, FAKE, 1024, None) == _lib.BSG_ERR_DTYPE
+    assert lib.bsg_select_topk_l1(FAKE, 4096, 16, 4096, 8, FAKE, FAKE, 0, FAKE, 16, None) == _lib.BSG_ERR_WORKSPACE
+    assert lib.bsg_select_topk_l1(FAKE, 4096, 16, 4096, -1, FAKE, FAKE, 0, FAKE, 1024, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_pack_weight(FAKE, 16, 64, 64, 1, 0, FAKE, 8, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_workspace_init(None, 64, None) == _lib.BSG_ERR_ARG
+
+
+def test_status_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.BSG_ERR_ARG)
+    with pytest.raises(TypeError):
+        _lib.check(_lib.BSG_ERR_DTYPE)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.BSG_ERR_UNSUPPORTED)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.BSG_ERR_HIP)
+    _lib.check(0)
+
+
+def test_kernel_tiles_and_config_shims():
+    tiles = bsa.kernel_tiles()
+    assert (16, 32, 4, 4) in tiles and (64, 64, 4, 2) in tiles
+    from bsa_mi355x import runtime
+
+    cfgs = runtime._PREPACK_AUTOTUNE_CONFIGS
+    assert len(cfgs) == len(tiles)
+    assert {"BLOCK_B", "BLOCK_N"} <= set(cfgs[0].kwargs) and cfgs[0].num_warps >= 1 and cfgs[0].num_stages >= 1
+
+
+def test_make_plan_maps_reference_tiles():
+    p = bsa.make_plan(4, 16, 64, 2, 3, bt=64)
+    assert p.as_tuple() == (4, 64, 2, 4, 64)   # BLOCK_B raised to cover the batch; stages -> depth 4
+    assert bsa.make_plan().as_tuple() == (0, 0, 0, 0, 0)
+    assert bsa.n_keep_for_density(0.48, 64) == 31

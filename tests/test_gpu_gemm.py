@@ -1,0 +1,246 @@
+"""GPU parity of the block-sparse GEMM (HIP, gfx950) against the CPU oracle.
+
+Bar (BASELINE): relative Frobenius error <= 1e-3 and max-abs error <= 1e-2 * max|Y_ref| for
+fp16 inputs with fp32 accumulation; the reference is oracle.bsg_oracle.gemm_ref64 (gather +
+matmul in float64) or gemm_ref (float32, BASELINE's CPU path) at full Llama sizes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import bsa_mi355x as bsa
+from helpers import assert_close, case, to_dev
+from oracle import bsg_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+F16 = torch.float16
+
+
+def _run_list(dev, x, w_nk, idx, plan=None, prefix="t", sort=True, dtype=F16):
+    bt, k = x.shape
+    n = w_nk.shape[0]
+    xt = to_dev(x, dev, dtype).view(bt, 1, k)
+    wt = to_dev(w_nk, dev, dtype)
+    it = to_dev(np.asarray(idx, dtype=np.int32), dev)
+    out = torch.full((bt, 1, n), float("nan"), dtype=dtype, device=dev)
+    if plan is None:
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(xt, wt, it, out, cache_prefix=prefix,
+                                                            sort_active_blocks=sort)
+    else:
+        bsa._prepacked_block_sparse_gemm_from_active_blocks_splitk(xt, wt, it, out, cache_prefix=prefix, **plan)
+    torch.cuda.synchronize()
+    return out.view(bt, n).float().cpu().numpy()
+
+
+@pytest.mark.parametrize("bt,k,n,na", [
+    (1, 64, 16, 1),
+    (2, 128, 32, 1),
+    (3, 256, 48, 2),
+    (16, 1024, 256, 8),
+    (17, 512, 100, 5),      # N not a multiple of 16, bt not a multiple of 16
+    (33, 2048, 520, 13),
+    (64, 4096, 1024, 31),
+    (100, 1024, 384, 9),    # bt above 64 rows: more grid rows
+])
+def test_small_shapes(dev, bt, k, n, na):
+    x, w_nk, idx = case(100 + bt, bt, k, n, na)
+    y = _run_list(dev, x, w_nk, idx, prefix=f"small{bt}")
+    assert_close(y, orc.gemm_ref64(x, w_nk, idx), f"bt={bt} k={k} n={n} na={na}")
+
+
+def test_k_tail_block(dev):
+    """K not a multiple of 64: the last block is partial (reference masks rk < M, KRN:709-717)."""
+    bt, k, n = 5, 1000, 64
+    nb = orc.nblk_of(k)
+    x, w_nk, _ = case(7, bt, k, n, 1)
+    idx = np.array([0, 3, nb - 1], dtype=np.int32)
+    assert_close(_run_list(dev, x, w_nk, idx, prefix="ktail"), orc.gemm_ref64(x, w_nk, idx), "k tail")
+
+
+def test_k_not_multiple_of_8(dev):
+    bt, k, n = 3, 203, 32
+    x, w_nk, _ = case(8, bt, k, n, 1)
+    idx = np.array([1, 3], dtype=np.int32)
+    assert_close(_run_list(dev, x, w_nk, idx, prefix="k203"), orc.gemm_ref64(x, w_nk, idx), "k=203")
+
+
+def test_zero_active_writes_zeros(dev):
+    x, w_nk, _ = case(9, 4, 256, 64, 1)
+    xt = to_dev(x, dev).view(4, 1, 256)
+    wt = to_dev(w_nk, dev)
+    out = torch.full((4, 1, 64), 7.0, dtype=F16, device=dev)
+    bsa._prepacked_block_sparse_gemm_from_active_blocks(xt, wt, torch.empty(0, dtype=torch.int32, device=dev), out)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+
+
+def test_out_of_range_ids_contribute_nothing(dev):
+    bt, k, n = 4, 512, 64
+    x, w_nk, _ = case(10, bt, k, n, 1)
+    idx = np.array([1, 8, 5, 1000, -3], dtype=np.int32)  # nblk = 8: ids 8, 1000, -3 are outside
+    y = _run_list(dev, x, w_nk, idx, prefix="oor", sort=False)
+    assert_close(y, orc.gemm_ref64(x, w_nk, [1, 5]), "out-of-range ids")
+
+
+def test_unsorted_list_and_limit(dev):
+    bt, k, n = 8, 1024, 128
+    x, w_nk, _ = case(11, bt, k, n, 1)
+    idx = np.array([9, 2, 15, 4, 11, 0], dtype=np.int32)
+    y = _run_list(dev, x, w_nk, idx, prefix="unsorted", sort=False)
+    assert_close(y, orc.gemm_ref64(x, w_nk, idx), "unsorted")
+    xt = to_dev(x, dev).view(bt, 1, k)
+    out = torch.empty(bt, 1, n, dtype=F16, device=dev)
+    bsa._prepacked_block_sparse_gemm_from_active_blocks(xt, to_dev(w_nk, dev), to_dev(idx, dev), out,
+                                                        cache_prefix="limit", active_blocks_limit=3)
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx[:3]), "active_blocks_limit")
+
+
+def test_duplicate_ids_accumulate_twice(dev):
+    """A list entry is one accumulation (the naive kernel loops over list entries, KRN:708)."""
+    bt, k, n = 4, 512, 64
+    x, w_nk, _ = case(12, bt, k, n, 1)
+    idx = np.array([3, 3, 6], dtype=np.int32)
+    y = _run_list(dev, x, w_nk, idx, prefix="dup", sort=False)
+    ref = orc.gemm_ref64(x, w_nk, [3]) * 2 + orc.gemm_ref64(x, w_nk, [6])
+    assert_close(y, ref, "duplicates")
+
+
+def test_every_instantiated_tile(dev):
+    """Every compiled (rows, cols, waves, depth) kernel, split-K 1 and 3, fp16 and bf16."""
+    bt, k, n, na = 37, 4096, 1000, 29
+    x, w_nk, idx = case(13, bt, k, n, na)
+    ref = orc.gemm_ref64(x, w_nk, idx)
+    xb = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    wb = torch.from_numpy(w_nk.astype(np.float32)).to(torch.bfloat16)
+    ref_bf = orc.gemm_ref64(xb.float().numpy(), wb.float().numpy(), idx)
+    tiles = bsa.kernel_tiles()
+    assert len(tiles) >= 40
+    xt = to_dev(x, dev)
+    it = to_dev(idx, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    packed_b = bsa.pack_weight(wb.to(dev))
+    for rows, cols, waves, depth in tiles:
+        for sk in (1, 3):
+            # explicit plan through gemm_packed, so rows_per_group is honoured even when < bt
+            out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+            p = bsa.Plan(sk, cols, waves, depth, rows)
+            print(f"tile rows={rows} cols={cols} waves={waves} depth={depth} split_k={sk}", flush=True)
+            bsa.gemm_packed(xt, packed, n, it, out, plan=p, workspace_prefix="tiles")
+            torch.cuda.synchronize()
+            assert_close(out.float().cpu().numpy(), ref, f"tile {rows},{cols},{waves},{depth} sk={sk}")
+        # bf16 once per tile (split-K 2)
+        out_b = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
+        bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b, plan=bsa.Plan(2, cols, waves, depth, rows),
+                        workspace_prefix="tiles_bf")
+        torch.cuda.synchronize()
+        yb = out_b.float().cpu().numpy()
+        # bf16 output keeps 8 significant bits: tolerance 5e-3 rel. Frobenius, 2e-2 max-abs
+        rf = orc.rel_frobenius(yb, ref_bf)
+        assert rf <= 5e-3 and np.max(np.abs(yb - ref_bf)) <= 2e-2 * np.max(np.abs(ref_bf)), \
+            f"bf16 tile {rows},{cols},{waves},{depth}: rel_fro={rf:.3e}"
+
+
+@pytest.mark.parametrize("split_k", [1, 2, 4, 7, 16, 29])
+def test_split_k_factors(dev, split_k):
+    bt, k, n, na = 16, 11008, 4096, 86
+    x, w_nk, idx = case(1234, bt, k, n, na)
+    y = _run_list(dev, x, w_nk, idx, plan=dict(num_split_k=split_k), prefix=f"sk{split_k}")
+    assert_close(y, orc.gemm_ref(x, w_nk, idx), f"split_k={split_k}")
+
+
+def test_bitmap_and_dense_paths(dev):
+    bt, k, n, na = 16, 4096, 2048, 23
+    x, w_nk, idx = case(14, bt, k, n, na)
+    nb = orc.nblk_of(k)
+    xt = to_dev(x, dev).view(bt, 1, k)
+    wt = to_dev(w_nk, dev)
+    it = to_dev(idx, dev)
+    out = torch.empty(bt, 1, n, dtype=F16, device=dev)
+    bm = bsa._build_active_k_bitmap(it, nb, dev)
+    assert np.array_equal(bm.cpu().numpy(), orc.bitmap_from_list(idx, nb))
+    bsa._prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload(xt, wt, it, out, total_k_blocks=nb,
+                                                                        prebuilt_bitmap=bm)
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx), "bitmap")
+    bsa._prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload_splitk(xt, wt, it, out, total_k_blocks=nb,
+                                                                               prebuilt_bitmap=bm, num_split_k=4)
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx), "bitmap split-K")
+    # a shorter bitmap than ceil(K/64): later blocks are inactive
+    bsa._prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload(xt, wt, it, out, total_k_blocks=40,
+                                                                        prebuilt_bitmap=bm[:40].contiguous())
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx[idx < 40]), "short bitmap")
+    bsa.dense_gemm(xt, wt, out)
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.arange(nb)), "dense")
+
+
+def test_device_count(dev):
+    """List capacity 40, device-side count 17: only the first 17 entries count."""
+    bt, k, n = 16, 4096, 512
+    x, w_nk, _ = case(15, bt, k, n, 1)
+    rng = np.random.default_rng(3)
+    idx = rng.permutation(64)[:40].astype(np.int32)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    out = torch.empty(bt, n, dtype=F16, device=dev)
+    cnt = torch.tensor([17], dtype=torch.int32, device=dev)
+    bsa.gemm_packed(to_dev(x, dev), packed, n, to_dev(idx, dev), out, num_active=40, num_active_dev=cnt)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx[:17]), "device count")
+
+
+def test_pack_layout_bit_exact(dev):
+    """Device packing == oracle tile_permute(pack_kmajor(W)) bit for bit (both layouts)."""
+    for n, k in ((100, 1000), (4096, 256), (48, 64)):
+        rng = np.random.default_rng(n + k)
+        w_nk = rng.normal(0, 0.02, size=(n, k)).astype(np.float16)
+        want = orc.tile_permute(orc.pack_kmajor(w_nk))
+        got = bsa.pack_weight(to_dev(w_nk, dev)).cpu().numpy()
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), (n, k)
+        got_kn = bsa.pack_weight(to_dev(np.ascontiguousarray(w_nk.T), dev), layout="kn").cpu().numpy()
+        assert np.array_equal(got_kn.view(np.uint16), want.view(np.uint16)), (n, k, "kn")
+
+
+def test_deterministic_repeats(dev):
+    bt, k, n, na = 16, 11008, 4096, 62
+    x, w_nk, idx = case(16, bt, k, n, na)
+    a = _run_list(dev, x, w_nk, idx, plan=dict(num_split_k=8), prefix="det")
+    b = _run_list(dev, x, w_nk, idx, plan=dict(num_split_k=8), prefix="det")
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+LLAMA = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
+
+
+@pytest.mark.parametrize("bt,s", [(2, 0.803), (16, 0.638), (64, 0.520)])
+@pytest.mark.parametrize("shape", ["qkvo", "gate_up", "down"])
+def test_llama_shapes(dev, shape, bt, s):
+    """every Llama-2-7B projection shape at its batch/sparsity pair."""
+    k, n = LLAMA[shape]
+    nb = orc.nblk_of(k)
+    na = orc.n_active_for_sparsity(s, nb)
+    x, w_nk, idx = case(1234, bt, k, n, na, "laplace" if shape == "down" else "normal")
+    assert_close(_run_list(dev, x, w_nk, idx, prefix=f"llama_{shape}"), orc.gemm_ref(x, w_nk, idx),
+                 f"{shape} B={bt} s={s}")
+
+
+@pytest.mark.parametrize("s", [0.0, 0.25, 0.5, 0.638, 0.8])
+def test_down_proj_sparsity_sweep(dev, s):
+    """down_proj B=16 over the sparsity sweep (0 runs the dense path)."""
+    k, n, bt = 11008, 4096, 16
+    na = orc.n_active_for_sparsity(s, 172)
+    x, w_nk, idx = case(1234, bt, k, n, na)
+    if s == 0.0:
+        xt = to_dev(x, dev).view(bt, 1, k)
+        out = torch.empty(bt, 1, n, dtype=F16, device=dev)
+        bsa.dense_gemm(xt, to_dev(w_nk, dev), out)
+        torch.cuda.synchronize()
+        y = out.view(bt, n).float().cpu().numpy()
+    else:
+        y = _run_list(dev, x, w_nk, idx, prefix="sweep")
+    assert_close(y, orc.gemm_ref(x, w_nk, idx), f"down s={s}")

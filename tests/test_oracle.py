@@ -1,0 +1,175 @@
+"""Pins the CPU oracle (no GPU): golden fixtures written by independent pure-Python loops,
+closed forms, special cases and brute force, chosen so that a dropped term, a wrong index or a
+transposed operand fails at least one of them."""
+from __future__ import annotations
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bsg_oracle as orc
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "gemm_*.npz"))))
+def test_gemm_matches_golden_loops(path):
+    d = np.load(path)
+    y = orc.gemm_ref64(d["x"], d["w_nk"], d["idx"])
+    np.testing.assert_allclose(y, d["y"], rtol=1e-12, atol=1e-12)
+    y32 = orc.gemm_ref(d["x"], d["w_nk"], d["idx"])
+    assert orc.within_tolerance(y32, d["y"]) or not np.any(d["y"])
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "select_*.npz"))))
+def test_select_matches_golden_loops(path):
+    d = np.load(path)
+    assert np.array_equal(orc.select_topk_l1(d["x"], int(d["k"])), d["sel"])
+    # exact integer scores equal the fp64 sums (fp16 |x| * 2^24 are exact integers)
+    np.testing.assert_array_equal(orc.l1_scores(d["x"]).astype(np.float64), d["scores"] * 2.0 ** 24)
+
+
+def test_golden_count():
+    assert len(glob.glob(os.path.join(GOLDEN, "*.npz"))) >= 7
+
+
+def test_pack_kmajor_closed_form():
+    rng = np.random.default_rng(0)
+    for n, k in ((5, 64), (7, 100), (16, 129)):
+        w = rng.normal(size=(n, k)).astype(np.float16)
+        wp = orc.pack_kmajor(w)
+        nb = orc.nblk_of(k)
+        assert wp.shape == (nb, 64, n)
+        for j in range(nb):
+            for c in range(64):
+                kk = 64 * j + c
+                want = w[:, kk] if kk < k else np.zeros(n, np.float16)
+                assert np.array_equal(wp[j, c], want)
+
+
+def test_tile_permute_index_formula_and_inverse():
+    rng = np.random.default_rng(1)
+    n, k = 40, 130
+    w = rng.normal(size=(n, k)).astype(np.float16)
+    ref = orc.pack_kmajor(w)
+    t = orc.tile_permute(ref)
+    npad = 48
+    assert t.shape == (orc.nblk_of(k), npad // 16, 1024)
+    flat = t.reshape(-1)
+    for j in range(ref.shape[0]):
+        for kk in range(64):
+            for nn in range(npad):
+                h, g, e = kk // 32, (kk % 32) // 8, kk % 8
+                tt, c = nn // 16, nn % 16
+                off = j * 64 * npad + tt * 1024 + h * 512 + g * 128 + c * 8 + e
+                want = ref[j, kk, nn] if nn < n else 0
+                assert flat[off] == want
+    assert np.array_equal(orc.tile_unpermute(t, n), ref)
+
+
+def test_gemm_dense_special_case():
+    rng = np.random.default_rng(2)
+    x = rng.normal(size=(3, 200)).astype(np.float16)
+    w = rng.normal(size=(9, 200)).astype(np.float16)
+    y = orc.gemm_ref64(x, w, np.arange(orc.nblk_of(200)))
+    np.testing.assert_allclose(y, x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_single_block_and_empty():
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(4, 256)).astype(np.float16)
+    w = rng.normal(size=(6, 256)).astype(np.float16)
+    y = orc.gemm_ref64(x, w, [2])
+    np.testing.assert_allclose(y, x[:, 128:192].astype(np.float64) @ w[:, 128:192].astype(np.float64).T)
+    assert not np.any(orc.gemm_ref64(x, w, []))
+    assert not np.any(orc.gemm_ref(x, w, [4, 7, -1]))  # nblk = 4: all out of range
+
+
+def test_gemm_permutation_invariance_and_not_transposed():
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(5, 512)).astype(np.float16)
+    w = rng.normal(size=(11, 512)).astype(np.float16)
+    a = orc.gemm_ref64(x, w, [1, 4, 6])
+    b = orc.gemm_ref64(x, w, [6, 1, 4])
+    np.testing.assert_allclose(a, b, rtol=1e-12)
+    assert a.shape == (5, 11)
+    # one-hot activation picks a weight column: catches a transposed operand
+    xo = np.zeros((1, 512), np.float16)
+    xo[0, 64 * 4 + 3] = 1
+    np.testing.assert_array_equal(orc.gemm_ref64(xo, w, [4])[0], w[:, 64 * 4 + 3].astype(np.float64))
+
+
+def test_gemm_ref_torch_matches_numpy():
+    x, w_kn, idx = orc.make_inputs(1234, 16, 1024, 256, "laplace", na=7)
+    yt = orc.gemm_ref_torch(torch.from_numpy(x), torch.from_numpy(w_kn), torch.from_numpy(idx.astype(np.int64)))
+    y = orc.gemm_ref64(x, np.ascontiguousarray(w_kn.T), idx)
+    assert orc.within_tolerance(yt.numpy(), y)
+
+
+def test_bitmap_round_trip():
+    idx = np.array([5, 1, 9], np.int32)
+    bm = orc.bitmap_from_list(idx, 12)
+    assert bm.dtype == np.uint8 and bm.sum() == 3
+    assert np.array_equal(orc.list_from_bitmap(bm), [1, 5, 9])
+
+
+def test_f16_units_exact():
+    vals = np.array([0.0, -0.0, 2 ** -24, 2 ** -14, 1.0, -1.5, 65504.0, 3.140625], dtype=np.float16)
+    u = orc.f16_units(vals)
+    np.testing.assert_array_equal(u.astype(np.float64), np.abs(vals.astype(np.float64)) * 2.0 ** 24)
+    inf_nan = orc.f16_units(np.array([np.inf, np.nan], dtype=np.float16))
+    assert inf_nan[0] > orc.f16_units(np.array([65504.0], np.float16))[0] and inf_nan[1] > inf_nan[0]
+
+
+def test_l1_scores_brute_force():
+    rng = np.random.default_rng(6)
+    x = rng.laplace(0, 0.05, size=(3, 200)).astype(np.float16)
+    s = orc.l1_scores(x)
+    for j in range(4):
+        want = sum(int(v) for v in orc.f16_units(x[:, 64 * j:min(64 * j + 64, 200)]).reshape(-1))
+        assert int(s[j]) == want
+
+
+def test_select_tie_rule_and_topk_agreement():
+    x = np.zeros((2, 64 * 6), np.float16)
+    x[:, 64 * 2:64 * 3] = 1.0
+    x[:, 64 * 4:64 * 5] = 1.0
+    x[:, 64 * 5:64 * 6] = 2.0
+    assert np.array_equal(orc.select_topk_l1(x, 2), [2, 5])   # 5 strongest, then 2 beats 4 on id
+    assert np.array_equal(orc.select_topk_l1(x, 4), [0, 2, 4, 5])
+    assert np.array_equal(orc.select_topk_l1(np.zeros((1, 640), np.float16), 3), [0, 1, 2])
+    # distinct scores: agrees with torch.topk on CPU
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(16, 4096)).astype(np.float16)
+    s = torch.from_numpy(orc.l1_scores(x).astype(np.float64))
+    assert len(set(s.tolist())) == s.numel()
+    want = torch.topk(s, 23).indices.sort()[0].numpy()
+    assert np.array_equal(orc.select_topk_l1(x, 23), want)
+
+
+def test_n_keep_and_baseline_pairs():
+    assert orc.n_keep(0.48, 64) == 31                # config 4: k=31 at ~0.52 sparsity
+    assert orc.n_active_for_sparsity(0.5, 172) == 86  # config 1
+    assert [orc.n_active_for_sparsity(s, 172) for s in (0, 0.25, 0.5, 0.638, 0.8)] == [172, 129, 86, 62, 34]
+    assert [orc.n_active_for_sparsity(s, 64) for s in (0.803, 0.638, 0.520)] == [13, 23, 31]
+    assert orc.n_keep(0.0, 64) == 1 and orc.n_keep(2.0, 64) == 64
+
+
+def test_l2_mean_selector_reference_semantics():
+    rng = np.random.default_rng(8)
+    x = rng.normal(size=(4, 1000)).astype(np.float16)  # floor(1000/64) = 15 blocks
+    got = orc.select_l2_mean_ref(x, 0.5)
+    xb = torch.from_numpy(x[:, :960].astype(np.float32)).reshape(-1, 15, 64)
+    want = torch.topk(xb.norm(dim=2).mean(dim=0), k=8).indices.sort()[0].numpy()
+    assert np.array_equal(got, want)
+
+
+def test_make_inputs_seeded():
+    a = orc.make_inputs(1234, 2, 128, 32, "normal", na=1)
+    b = orc.make_inputs(1234, 2, 128, 32, "normal", na=1)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+    assert a[1].shape == (128, 32) and a[0].dtype == np.float16 and a[2].dtype == np.int32

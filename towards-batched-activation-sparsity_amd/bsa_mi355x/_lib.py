@@ -1,0 +1,136 @@
+"""ctypes binding of libbsgemm.so (C ABI declared in include/bsgemm.h).
+
+The library is loaded after torch so that its libamdhip64.so.7 dependency resolves to the
+HIP runtime torch already mapped (same SONAME): device pointers and hipStream_t handles
+taken from torch tensors and streams are then valid inside the library.
+There is no fallback: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libbsgemm.so")
+
+BSG_OK = 0
+BSG_ERR_ARG = -1
+BSG_ERR_DTYPE = -2
+BSG_ERR_WORKSPACE = -3
+BSG_ERR_ALIGN = -4
+BSG_ERR_UNSUPPORTED = -5
+BSG_ERR_HIP = -100
+
+BSG_F16 = 0
+BSG_BF16 = 1
+BLOCK_K = 64
+MAX_NBLK = 2048
+
+
+class BsgError(RuntimeError):
+    """A libbsgemm call returned a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"libbsgemm status {status}: {message}")
+        self.status = status
+
+
+class BsgArgError(BsgError, ValueError):
+    pass
+
+
+class BsgDtypeError(BsgError, TypeError):
+    pass
+
+
+class BsgUnsupported(BsgError, NotImplementedError):
+    pass
+
+
+class Plan(ctypes.Structure):
+    """Mirror of `bsg_plan`; zero fields are resolved by the library."""
+
+    _fields_ = [
+        ("split_k", ctypes.c_int32),
+        ("cols_per_wave", ctypes.c_int32),
+        ("waves_per_group", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("rows_per_group", ctypes.c_int32),
+    ]
+
+    def as_tuple(self):
+        return (self.split_k, self.cols_per_wave, self.waves_per_group, self.depth, self.rows_per_group)
+
+    def __repr__(self) -> str:
+        return ("Plan(split_k=%d, cols_per_wave=%d, waves_per_group=%d, depth=%d, rows_per_group=%d)"
+                % self.as_tuple())
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_int = ctypes.c_int
+_pplan = ctypes.POINTER(Plan)
+
+# name -> (restype, argtypes); every function declared in include/bsgemm.h
+SIGNATURES = {
+    "bsg_version": (ctypes.c_char_p, []),
+    "bsg_last_error": (ctypes.c_char_p, []),
+    "bsg_packed_bytes": (_i64, [_i64, _i64, _int]),
+    "bsg_pack_weight": (_int, [_vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp]),
+    "bsg_plan_resolve": (_int, [_i64, _i64, _i32, _i32, _i32, _pplan]),
+    "bsg_gemm_workspace_bytes": (_i64, [_i64, _i64, _pplan]),
+    "bsg_workspace_init": (_int, [_vp, _i64, _vp]),
+    "bsg_gemm": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
+    "bsg_gemm_bitmap": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
+    "bsg_gemm_dense": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
+    "bsg_select_workspace_bytes": (_i64, [_i64]),
+    "bsg_select_topk_l1": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _int, _vp, _i64, _vp]),
+    "bsg_select_gemm": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _i64,
+                               _pplan, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Load (once) and return the ctypes library handle."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (maps torch's libamdhip64.so.7 first)
+
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"HIP library not built: {LIB_PATH} is missing. Build it with "
+                "`python towards-batched-activation-sparsity_amd/build.py` or __graft_entry__.build().")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().bsg_last_error().decode("utf-8", "replace")
+
+
+def check(status: int) -> None:
+    """Raise the Python exception matching a libbsgemm status."""
+    if status == BSG_OK:
+        return
+    msg = last_error()
+    if status in (BSG_ERR_ARG, BSG_ERR_ALIGN):
+        raise BsgArgError(status, msg)
+    if status == BSG_ERR_DTYPE:
+        raise BsgDtypeError(status, msg)
+    if status == BSG_ERR_UNSUPPORTED:
+        raise BsgUnsupported(status, msg)
+    raise BsgError(status, msg)

@@ -1,0 +1,874 @@
+// bsgemm.hip — gfx950 (MI355X / CDNA4) kernels and C ABI for the batch-shared
+// 64-channel block-sparse GEMM  Y[bt,N] = sum_{j active} X[bt,64j:64j+64] · W[64j:64j+64,N].
+//
+// Reference semantics: kernels/shared_mask_batched_triton_min_runtime.py
+//   naive list kernel 684-733, bitmap kernel 814-874, split-K write/reduce 1898-1988,
+//   packing 3133-3163, host wrappers 1064-1454 and 3166-3344.
+//
+// Design (MI355X-first, not a translation of the Triton kernels):
+//   * The weight is packed once into a tiled K-major layout (see include/bsgemm.h): each
+//     K-block is a contiguous slab and each 16-column tile of it is a 2 KiB run that a single
+//     64-lane dwordx4 buffer load per k-half delivers straight into the A operand of
+//     v_mfma_f32_16x16x32_{f16,bf16}.  No LDS staging of W, no transposes.
+//   * The batch tile (16/32/64 rows) is the MFMA B operand, read with 16-byte loads from X
+//     (tiny, L2-resident).  Rows >= bt, blocks past the list and k >= K are turned into
+//     out-of-range buffer offsets, which return zeros without touching memory.
+//   * Each work-group owns cols_per_wave output columns.  Its waves split the active-block
+//     list into contiguous slices (in-group split-K, reduced through LDS in wave order), and
+//     split_k work-groups share one column tile (fp32 partials + arrival counter; the last
+//     work-group to arrive sums the partials in split order, so results are run-to-run
+//     deterministic and a single launch suffices — no second reduce kernel).
+//   * Every wave keeps `depth` K-blocks of loads in flight (a rolling register pipeline);
+//     block ids come from LDS and are made wave-uniform, so buffer descriptors are scalar.
+//   * The work-group -> tile map is XCD-aware: consecutive logical work-groups land on the
+//     same XCD, so the split_k partners of a tile share one L2.
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "bsgemm.h"
+
+#define BSG_VERSION_STR "bsgemm 0.1 (gfx950, mfma_f32_16x16x32)"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(BSG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kOOB = (int)0x80000000u;  // buffer offset beyond any num_records we build
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2 };
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+}
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<_Float16> {
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+};
+
+template <>
+struct Elem<__bf16> {
+  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+  }
+};
+
+// Exclusive prefix sum over the work-group; also returns the total.  `scratch` holds
+// one int per wave.  Contains two barriers.
+template <int NT>
+__device__ __forceinline__ int wg_exclusive_scan(int v, int* scratch, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) scratch[w] = incl;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) {
+    int s = scratch[i];
+    if (i < w) base += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + incl - v;
+}
+
+// Split-K hand-off primitives.  BSG_SPLITK_FENCES=1 selects full agent-scope fences
+// (L2 write-back + invalidate on every work-group); the default moves partials with
+// agent-scope relaxed atomics, which are device-coherent without touching the rest of L2.
+#ifndef BSG_SPLITK_FENCES
+#define BSG_SPLITK_FENCES 0
+#endif
+
+__device__ __forceinline__ void part_store(float* p, float v) {
+#if BSG_SPLITK_FENCES
+  *p = v;
+#else
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
+}
+
+__device__ __forceinline__ f32x4 part_load(const f32x4* p) {
+#if BSG_SPLITK_FENCES
+  return *p;
+#else
+  const float* q = (const float*)p;
+  f32x4 v;
+  v.x = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.y = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.z = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.w = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+#endif
+}
+
+// Every store of this wave has completed (at the scope it was issued with).
+__device__ __forceinline__ void part_publish() {
+#if BSG_SPLITK_FENCES
+  __threadfence();
+#else
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt(7), lgkmcnt(15)
+#endif
+}
+
+__device__ __forceinline__ void part_acquire() {
+#if BSG_SPLITK_FENCES
+  __threadfence();
+#endif
+}
+
+__device__ __forceinline__ unsigned counter_add(uint32_t* c) {
+  return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void counter_reset(uint32_t* c) {
+  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct GemmParams {
+  const void* x;
+  const void* wp;
+  void* y;
+  const int32_t* idx;
+  const int32_t* na_dev;
+  const uint8_t* bitmap;
+  float* part;
+  uint32_t* cnt;
+  int64_t ldx;
+  int64_t ldy;
+  int32_t bt, K, N, npad, nblk, nbm, na, mode, split_k, n_tiles, x_bytes, y_fast;
+};
+
+// One work-group: BTT*16 batch rows x NSUB*16 columns, WPG waves splitting its share of the
+// block list, DEPTH blocks of loads in flight per wave.
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
+__global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
+  constexpr int NT = 64 * WPG;
+  constexpr int F = BTT * NSUB;
+  constexpr int RED_BYTES = WPG > 1 ? (WPG - 1) * F * 64 * 16 : 0;  // waves 1..WPG-1
+  constexpr int IDS_BYTES = BSG_MAX_NBLK * 4;
+  // The block list (main loop) and the wave-reduction buffer (epilogue) share LDS.
+  __shared__ __attribute__((aligned(16))) char s_mem[RED_BYTES > IDS_BYTES ? RED_BYTES : IDS_BYTES];
+  __shared__ int s_misc[WPG + 2];
+  int* const s_ids = (int*)s_mem;
+  f32x4* const s_red = (f32x4*)s_mem;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // XCD-aware work-group order: hardware places work-group b on XCD b % 8.
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int lid = (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
+  const int S = p.split_k;
+  const int tile = lid / S;
+  const int sk = lid - tile * S;
+  const int n0 = tile * (16 * NSUB);
+  const int y0 = blockIdx.y * (16 * BTT);
+
+  // 1. Stage this call's active-block list in LDS.
+  int na;
+  if (p.mode == MODE_LIST) {
+    na = p.na;
+    if (p.na_dev != nullptr) {
+      const int d = *p.na_dev;
+      na = d < 0 ? 0 : (d < na ? d : na);
+    }
+    for (int i = tid; i < na; i += NT) s_ids[i] = p.idx[i];
+  } else if (p.mode == MODE_BITMAP) {
+    const int per = (p.nbm + NT - 1) / NT;
+    const int beg = tid * per < p.nbm ? tid * per : p.nbm;
+    const int end = beg + per < p.nbm ? beg + per : p.nbm;
+    int c = 0;
+    for (int i = beg; i < end; ++i) c += p.bitmap[i] != 0;
+    int total = 0;
+    int o = wg_exclusive_scan<NT>(c, s_misc, &total);
+    for (int i = beg; i < end; ++i)
+      if (p.bitmap[i] != 0) s_ids[o++] = i;
+    na = total;
+  } else {
+    na = p.nblk;
+    for (int i = tid; i < na; i += NT) s_ids[i] = i;
+  }
+  na = __builtin_amdgcn_readfirstlane(na);
+  __syncthreads();
+
+  // 2. This wave's contiguous slice [pbeg, pend) of the list.
+  const int G = S * WPG;
+  const int g = sk * WPG + w;
+  const int pbeg = (int)(((int64_t)na * g) / G);
+  const int pend = (int)(((int64_t)na * (g + 1)) / G);
+  const int cnt = pend - pbeg;
+
+  const int blk_bytes = p.npad * 128;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  int xrow_off[BTT];
+  bool xrow_ok[BTT];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi) {
+    const int row = y0 + 16 * bi + (lane & 15);
+    xrow_ok[bi] = row < p.bt;
+    xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
+  }
+  const int xcol = 8 * (lane >> 4);
+  const int wcol = lane * 16 + (n0 >> 4) * 2048;
+
+  u32x4 wv[DEPTH][NSUB][2];
+  u32x4 xv[DEPTH][BTT][2];
+  f32x4 acc[BTT][NSUB];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](u32x4 (&wd)[NSUB][2], u32x4 (&xd)[BTT][2], int t) {
+    const int q = t < cnt ? pbeg + t : 0;
+    int blk = s_ids[q];
+    blk = __builtin_amdgcn_readfirstlane(blk);
+    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      wd[s][0] = ld16(wr, wcol + s * 2048);
+      wd[s][1] = ld16(wr, wcol + s * 2048 + 1024);
+    }
+    const int kb = (ok ? blk : 0) * 64 + xcol;
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int col = kb + 32 * h;
+        const bool v = ok && xrow_ok[bi] && col < p.K;
+        xd[bi][h] = ld16(xr, v ? xrow_off[bi] + col * 2 : kOOB);
+      }
+    }
+  };
+
+  auto compute = [&](const u32x4 (&wd)[NSUB][2], const u32x4 (&xd)[BTT][2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][h], xd[bi][h], acc[bi][s]);
+  };
+
+  // 3. Rolling pipeline: DEPTH blocks in flight; loads past the slice are out-of-range
+  //    (zero, no memory traffic) so the body has no data-dependent branches.
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
+  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(wv[d], xv[d]);
+      issue(wv[d], xv[d], t0 + d + DEPTH);
+    }
+  }
+
+  // 4. Output.  Fragment f = (bi, s): lane holds Y[y0+16bi+lane%16][n0+16s+4(lane/16)+r].
+  auto store_y = [&](int f, f32x4 v) {
+    const int bi = f / NSUB;
+    const int s = f - bi * NSUB;
+    const int b = y0 + 16 * bi + (lane & 15);
+    const int n = n0 + 16 * s + 4 * (lane >> 4);
+    if (b >= p.bt) return;
+    uint16_t* yrow = (uint16_t*)p.y + (size_t)b * (size_t)p.ldy;
+    if (p.y_fast) {
+      if (n < p.N) {
+        u32x2 pk;
+        pk.x = (uint32_t)Elem<T>::bits(v.x) | ((uint32_t)Elem<T>::bits(v.y) << 16);
+        pk.y = (uint32_t)Elem<T>::bits(v.z) | ((uint32_t)Elem<T>::bits(v.w) << 16);
+        *(u32x2*)(yrow + n) = pk;
+      }
+    } else {
+      if (n + 0 < p.N) yrow[n + 0] = Elem<T>::bits(v.x);
+      if (n + 1 < p.N) yrow[n + 1] = Elem<T>::bits(v.y);
+      if (n + 2 < p.N) yrow[n + 2] = Elem<T>::bits(v.z);
+      if (n + 3 < p.N) yrow[n + 3] = Elem<T>::bits(v.w);
+    }
+  };
+
+  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
+  f32x4* part = (f32x4*)p.part;
+  auto emit = [&](int f, f32x4 v) {
+    if (S == 1) {
+      store_y(f, v);
+    } else {
+      float* dst = (float*)&part[((tile_lin * S + sk) * F + f) * 64 + lane];
+      part_store(dst + 0, v.x);
+      part_store(dst + 1, v.y);
+      part_store(dst + 2, v.z);
+      part_store(dst + 3, v.w);
+    }
+  };
+
+  if constexpr (WPG > 1) {
+    // Waves 1..WPG-1 hand their accumulators to wave 0 through LDS; wave 0 sums in wave
+    // order and emits every fragment.
+    __syncthreads();  // every wave is done reading s_ids before s_red overwrites it
+    if (w > 0) {
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) s_red[((w - 1) * F + bi * NSUB + s) * 64 + lane] = acc[bi][s];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+          f32x4 v = acc[bi][s];
+          for (int ww = 1; ww < WPG; ++ww) v += s_red[((ww - 1) * F + bi * NSUB + s) * 64 + lane];
+          emit(bi * NSUB + s, v);
+        }
+    }
+  } else {
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
+  }
+
+  if (S > 1) {
+    // Publish the partial, count arrivals; the last work-group of the tile reduces in
+    // split order and re-arms the counter for the next launch (graph-replay safe).
+    // Partials move through agent-scope (device-coherent) stores and loads, so no L2
+    // write-back/invalidate is needed: each wave waits for its own stores to complete,
+    // the barrier orders them before the counter update, and the last work-group issues
+    // its loads only after it has seen the final count.
+    part_publish();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = counter_add(&p.cnt[tile_lin]);
+      s_misc[WPG] = prev == (unsigned)(S - 1);
+    }
+    __syncthreads();
+    if (s_misc[WPG]) {
+      part_acquire();
+      for (int f = w; f < F; f += WPG) {
+        f32x4 v = part_load(&part[((tile_lin * S) * F + f) * 64 + lane]);
+        for (int q = 1; q < S; ++q) v += part_load(&part[((tile_lin * S + q) * F + f) * 64 + lane]);
+        store_y(f, v);
+      }
+      if (tid == 0) counter_reset(&p.cnt[tile_lin]);
+    }
+  }
+}
+
+// Pack W (logical [N,K], element strides sn/sk) into the tiled K-major layout.
+// One thread per 8-element (16-byte) group of the packed slab.
+__global__ __launch_bounds__(256) void bsg_pack_kernel(const uint16_t* __restrict__ w, int64_t N,
+                                                       int64_t K, int64_t sn, int64_t skk,
+                                                       int64_t ntile, int64_t groups,
+                                                       uint16_t* __restrict__ wp) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= groups) return;
+  const int64_t blk = gid / (ntile * 128);
+  const int64_t rem = gid - blk * ntile * 128;
+  const int64_t t = rem >> 7;
+  const int r = (int)(rem & 127);
+  const int h = r >> 6, g = (r >> 4) & 3, c = r & 15;
+  const int64_t n = 16 * t + c;
+  const int64_t k0 = 64 * blk + 32 * h + 8 * g;
+  uint16_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (n < N && k0 + e < K) ? w[n * sn + (k0 + e) * skk] : (uint16_t)0;
+  u32x4 o;
+  o.x = v[0] | ((uint32_t)v[1] << 16);
+  o.y = v[2] | ((uint32_t)v[3] << 16);
+  o.z = v[4] | ((uint32_t)v[5] << 16);
+  o.w = v[6] | ((uint32_t)v[7] << 16);
+  *(u32x4*)(wp + gid * 8) = o;
+}
+
+__global__ __launch_bounds__(256) void bsg_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+// |x| of an fp16 value in units of 2^-24 (exact for every finite value; Inf/NaN map above
+// every finite value, NaN above Inf).
+__device__ __forceinline__ uint64_t f16_units(uint32_t hbits) {
+  const uint32_t b = hbits & 0x7fffu;
+  const uint32_t e = b >> 10, m = b & 0x3ffu;
+  return e == 0 ? (uint64_t)m : ((uint64_t)(1024u | m) << (e - 1));
+}
+
+struct SelParams {
+  const uint16_t* x;
+  int64_t ldx;
+  uint64_t* scores;
+  uint32_t* cnt;
+  int32_t* idx_out;
+  int32_t* na_out;
+  int32_t bt, K, nblk, k;
+};
+
+// Fused selector: work-group j scores block j; the last work-group to finish ranks all
+// blocks by (score desc, id asc), keeps the first k and writes them in ascending id order.
+__global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
+  __shared__ uint64_t s_sc[BSG_MAX_NBLK];
+  __shared__ uint64_t s_part[4];
+  __shared__ int s_scan[4];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = blockIdx.x;
+
+  uint64_t acc = 0;
+  const int groups = p.bt * 8;
+  for (int gi = tid; gi < groups; gi += 256) {
+    const int row = gi >> 3;
+    const int col = 64 * j + 8 * (gi & 7);
+    if (col < p.K) {
+      const u32x4 v = *(const u32x4*)(p.x + (size_t)row * (size_t)p.ldx + col);
+      acc += f16_units(v.x & 0xffffu) + f16_units(v.x >> 16) + f16_units(v.y & 0xffffu) +
+             f16_units(v.y >> 16) + f16_units(v.z & 0xffffu) + f16_units(v.z >> 16) +
+             f16_units(v.w & 0xffffu) + f16_units(v.w >> 16);
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
+  if (lane == 0) s_part[w] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    p.scores[j] = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+    __threadfence();
+    const unsigned prev = atomicAdd(p.cnt, 1u);
+    s_last = prev == (unsigned)(p.nblk - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  const int nb = p.nblk;
+  for (int i = tid; i < nb; i += 256) s_sc[i] = p.scores[i];
+  __syncthreads();
+  const int per = (nb + 255) / 256;
+  const int beg = tid * per < nb ? tid * per : nb;
+  const int end = beg + per < nb ? beg + per : nb;
+  const int k = p.k < nb ? p.k : nb;
+  // selected flags of this thread's chunk, packed into a 64-bit mask (per <= 8 here)
+  uint64_t selmask = 0;
+  int c = 0;
+  for (int jj = beg; jj < end; ++jj) {
+    const uint64_t sj = s_sc[jj];
+    int rank = 0;
+    for (int i = 0; i < nb; ++i) {
+      const uint64_t si = s_sc[i];
+      rank += (si > sj) || (si == sj && i < jj);
+    }
+    if (rank < k) {
+      selmask |= 1ull << (jj - beg);
+      ++c;
+    }
+  }
+  int total = 0;
+  int o = wg_exclusive_scan<256>(c, s_scan, &total);
+  for (int jj = beg; jj < end; ++jj)
+    if (selmask & (1ull << (jj - beg))) p.idx_out[o++] = jj;
+  if (tid == 0) {
+    *p.na_out = k;
+    *p.cnt = 0u;
+  }
+}
+
+// ----------------------------------------------------------------------------------------
+// Host side: kernel table, plan resolution, validation, launches.
+
+typedef void (*GemmFn)(GemmParams);
+
+struct KernelEntry {
+  int btt, nsub, wpg, depth;
+  GemmFn f16, bf16;
+};
+
+#define BSG_K(B, S, W, D) \
+  {B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
+
+// Instantiated tile set.  Register budget per lane ~ depth*(nsub+btt)*8 + btt*nsub*4.
+const KernelEntry kKernels[] = {
+    // 16 batch rows
+    BSG_K(1, 1, 1, 4), BSG_K(1, 1, 1, 8), BSG_K(1, 1, 2, 4), BSG_K(1, 1, 2, 8),
+    BSG_K(1, 1, 4, 2), BSG_K(1, 1, 4, 4), BSG_K(1, 1, 4, 8), BSG_K(1, 1, 8, 2),
+    BSG_K(1, 1, 8, 4), BSG_K(1, 1, 8, 8),
+    BSG_K(1, 2, 1, 4), BSG_K(1, 2, 1, 8), BSG_K(1, 2, 2, 4), BSG_K(1, 2, 2, 8),
+    BSG_K(1, 2, 4, 2), BSG_K(1, 2, 4, 4), BSG_K(1, 2, 4, 8), BSG_K(1, 2, 8, 2),
+    BSG_K(1, 2, 8, 4),
+    BSG_K(1, 4, 1, 4), BSG_K(1, 4, 2, 4), BSG_K(1, 4, 4, 2), BSG_K(1, 4, 4, 4),
+    BSG_K(1, 4, 8, 2),
+    BSG_K(1, 8, 1, 2), BSG_K(1, 8, 2, 2), BSG_K(1, 8, 4, 2),
+    // 32 batch rows
+    BSG_K(2, 2, 1, 4), BSG_K(2, 2, 2, 4), BSG_K(2, 2, 4, 2), BSG_K(2, 2, 4, 4),
+    BSG_K(2, 4, 1, 4), BSG_K(2, 4, 2, 2), BSG_K(2, 4, 2, 4), BSG_K(2, 4, 4, 2),
+    // 64 batch rows
+    BSG_K(4, 2, 1, 4), BSG_K(4, 2, 2, 2), BSG_K(4, 2, 2, 4), BSG_K(4, 2, 4, 2),
+    BSG_K(4, 4, 1, 2), BSG_K(4, 4, 1, 4), BSG_K(4, 4, 2, 2), BSG_K(4, 4, 4, 1),
+    BSG_K(4, 4, 4, 2),
+    BSG_K(4, 8, 1, 2), BSG_K(4, 8, 2, 1), BSG_K(4, 8, 2, 2),
+};
+#undef BSG_K
+
+const KernelEntry* find_kernel(int btt, int nsub, int wpg, int depth) {
+  for (const KernelEntry& e : kKernels)
+    if (e.btt == btt && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
+  return nullptr;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
+
+int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_plan* pl) {
+  if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
+    return fail(BSG_ERR_ARG, "plan: bt=%lld N=%lld nblk=%d na=%d cu=%d", (long long)bt, (long long)N,
+                nblk, na, cu);
+  if (pl->rows_per_group == 0) pl->rows_per_group = bt <= 16 ? 16 : (bt <= 32 ? 32 : 64);
+  const int rpg = pl->rows_per_group;
+  if (rpg != 16 && rpg != 32 && rpg != 64)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: rows_per_group=%d (16, 32 or 64)", rpg);
+  const int auto_fields = (pl->cols_per_wave == 0 ? 1 : 0) | (pl->waves_per_group == 0 ? 2 : 0) |
+                          (pl->depth == 0 ? 4 : 0);
+  if (pl->cols_per_wave == 0) pl->cols_per_wave = rpg == 16 ? 32 : 64;
+  if (pl->waves_per_group == 0) pl->waves_per_group = 4;
+  if (pl->depth == 0) pl->depth = rpg == 64 ? 2 : 4;
+  if (!pow2_in(pl->cols_per_wave, 16, 128) || !pow2_in(pl->waves_per_group, 1, 8) ||
+      !pow2_in(pl->depth, 1, 8))
+    return fail(BSG_ERR_UNSUPPORTED, "plan: cols_per_wave=%d waves_per_group=%d depth=%d",
+                pl->cols_per_wave, pl->waves_per_group, pl->depth);
+  if (!find_kernel(rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth) && auto_fields) {
+    // An automatic field led to a tile that is not compiled: take the instantiated kernel
+    // that keeps every explicit field and is closest in the automatic ones.
+    const KernelEntry* best = nullptr;
+    int best_d = 1 << 30;
+    for (const KernelEntry& e : kKernels) {
+      if (e.btt != rpg / 16) continue;
+      if (!(auto_fields & 1) && e.nsub * 16 != pl->cols_per_wave) continue;
+      if (!(auto_fields & 2) && e.wpg != pl->waves_per_group) continue;
+      if (!(auto_fields & 4) && e.depth != pl->depth) continue;
+      const int d = abs(e.nsub * 16 - pl->cols_per_wave) * 64 + abs(e.wpg - pl->waves_per_group) * 8 +
+                    abs(e.depth - pl->depth);
+      if (d < best_d) {
+        best_d = d;
+        best = &e;
+      }
+    }
+    if (best) {
+      pl->cols_per_wave = best->nsub * 16;
+      pl->waves_per_group = best->wpg;
+      pl->depth = best->depth;
+    }
+  }
+  if (!find_kernel(rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
+    return fail(BSG_ERR_UNSUPPORTED,
+                "plan: no kernel instantiated for rows_per_group=%d cols_per_wave=%d "
+                "waves_per_group=%d depth=%d",
+                rpg, pl->cols_per_wave, pl->waves_per_group, pl->depth);
+  if (pl->split_k == 0) {
+    const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, pl->cols_per_wave);
+    const int64_t groups = n_tiles * cdiv(bt, rpg);
+    const int64_t target = (int64_t)cu * 8;  // waves
+    int64_t s = cdiv(target, groups * pl->waves_per_group);
+    const int64_t by_work = (int64_t)na / (2 * pl->waves_per_group);  // >= 2 blocks per wave
+    if (s > by_work) s = by_work;
+    if (s > 32) s = 32;
+    if (s < 1) s = 1;
+    pl->split_k = (int32_t)s;
+  }
+  if (pl->split_k < 1 || pl->split_k > 256)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: split_k=%d (1..256)", pl->split_k);
+  return BSG_OK;
+}
+
+int64_t gemm_ws_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
+  if (pl->split_k <= 1) return 0;
+  const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, pl->cols_per_wave);
+  const int64_t tiles = n_tiles * cdiv(bt, pl->rows_per_group);
+  const int64_t frag = (int64_t)(pl->rows_per_group / 16) * (pl->cols_per_wave / 16);
+  const int64_t part = tiles * pl->split_k * frag * 64 * 16;
+  const int64_t counters = cdiv(tiles * 4, 256) * 256;
+  return counters + part;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Compute units of the current device, cached per device ordinal.
+int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+                 void* y, int64_t ldy, int dtype) {
+  if (dtype != BSG_F16 && dtype != BSG_BF16) return fail(BSG_ERR_DTYPE, "dtype=%d (0=fp16, 1=bf16)", dtype);
+  if (bt < 0 || K <= 0 || N <= 0) return fail(BSG_ERR_ARG, "sizes bt=%lld K=%lld N=%lld", (long long)bt, (long long)K, (long long)N);
+  if (cdiv(K, BSG_BLOCK_K) > BSG_MAX_NBLK)
+    return fail(BSG_ERR_UNSUPPORTED, "K=%lld exceeds %d blocks of 64", (long long)K, BSG_MAX_NBLK);
+  if (bt == 0) return BSG_OK;
+  if (!x || !wp || !y) return fail(BSG_ERR_ARG, "null pointer (x=%p wp=%p y=%p)", x, wp, y);
+  if (K % 8 != 0) return fail(BSG_ERR_ALIGN, "K=%lld must be a multiple of 8", (long long)K);
+  if (ldx < K || ldx % 8 != 0 || !aligned16(x))
+    return fail(BSG_ERR_ALIGN, "x must be 16-byte aligned with ldx >= K and ldx %% 8 == 0 (ldx=%lld)", (long long)ldx);
+  if (!aligned16(wp)) return fail(BSG_ERR_ALIGN, "packed weight must be 16-byte aligned");
+  if (ldy < N) return fail(BSG_ERR_ARG, "ldy=%lld < N=%lld", (long long)ldy, (long long)N);
+  if (((uintptr_t)y & 1u) != 0) return fail(BSG_ERR_ALIGN, "y must be 2-byte aligned");
+  if ((bt - 1) * ldx * 2 + ldx * 2 >= (int64_t)0x7fffffff)
+    return fail(BSG_ERR_UNSUPPORTED, "x spans >= 2 GiB");
+  if (cdiv(N, 16) * 16 * 128 >= (int64_t)0x7fffffff) return fail(BSG_ERR_UNSUPPORTED, "N too large");
+  return BSG_OK;
+}
+
+int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp,
+                int64_t N, const int32_t* idx, int32_t na, const int32_t* na_dev,
+                const uint8_t* bitmap, int32_t nbm, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
+                const bsg_plan* plan_in, void* stream) {
+  int rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype);
+  if (rc != BSG_OK || bt == 0) return rc;
+  const int32_t nblk = (int32_t)cdiv(K, BSG_BLOCK_K);
+  if (mode == MODE_LIST) {
+    if (na < 0 || na > BSG_MAX_NBLK) return fail(BSG_ERR_ARG, "num_active=%d (0..%d)", na, BSG_MAX_NBLK);
+    if (na > 0 && !idx) return fail(BSG_ERR_ARG, "active_blocks is null");
+  } else if (mode == MODE_BITMAP) {
+    if (!bitmap) return fail(BSG_ERR_ARG, "bitmap is null");
+    if (nbm < 1 || nbm > nblk)
+      return fail(BSG_ERR_ARG, "total_k_blocks=%d outside [1, ceil(K/64)=%d]", nbm, nblk);
+    na = nbm;
+  } else {
+    na = nblk;
+  }
+  bsg_plan pl = plan_in ? *plan_in : bsg_plan{0, 0, 0, 0, 0};
+  int cu = 256;
+  if (pl.split_k == 0) cu = device_cu_count();  // only feeds the automatic split-K choice
+  rc = resolve(bt, N, nblk, na, cu, &pl);
+  if (rc != BSG_OK) return rc;
+  const int64_t need = gemm_ws_bytes(bt, N, &pl);
+  if (need > 0 && !aligned16(ws)) return fail(BSG_ERR_ALIGN, "workspace must be 16-byte aligned");
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(BSG_ERR_WORKSPACE, "workspace %lld bytes < %lld needed (split_k=%d)", (long long)ws_bytes,
+                (long long)need, pl.split_k);
+  const KernelEntry* ke = find_kernel(pl.rows_per_group / 16, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
+  const int64_t npad = cdiv(N, 16) * 16;
+  const int64_t n_tiles = cdiv(npad, pl.cols_per_wave);
+  const int64_t ygroups = cdiv(bt, pl.rows_per_group);
+  if (n_tiles * pl.split_k > 0x7fffffff || ygroups > 65535) return fail(BSG_ERR_UNSUPPORTED, "grid too large");
+
+  GemmParams p;
+  p.x = x;
+  p.wp = wp;
+  p.y = y;
+  p.idx = idx;
+  p.na_dev = na_dev;
+  p.bitmap = bitmap;
+  const int64_t tiles = n_tiles * ygroups;
+  const int64_t cnt_bytes = cdiv(tiles * 4, 256) * 256;
+  p.cnt = need > 0 ? (uint32_t*)ws : nullptr;
+  p.part = need > 0 ? (float*)((char*)ws + cnt_bytes) : nullptr;
+  p.ldx = ldx;
+  p.ldy = ldy;
+  p.bt = (int32_t)bt;
+  p.K = (int32_t)K;
+  p.N = (int32_t)N;
+  p.npad = (int32_t)npad;
+  p.nblk = nblk;
+  p.nbm = nbm;
+  p.na = na;
+  p.mode = mode;
+  p.split_k = pl.split_k;
+  p.n_tiles = (int32_t)n_tiles;
+  p.x_bytes = (int32_t)(((bt - 1) * ldx + K) * 2);
+  p.y_fast = (N % 4 == 0) && (ldy % 4 == 0) && (((uintptr_t)y & 7u) == 0);
+
+  dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
+  dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
+  GemmFn fn = dtype == BSG_F16 ? ke->f16 : ke->bf16;
+  hipLaunchKernelGGL(fn, grid, block, 0, (hipStream_t)stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_gemm launch");
+  return BSG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bsg_version(void) { return BSG_VERSION_STR; }
+
+const char* bsg_last_error(void) { return g_err; }
+
+int64_t bsg_packed_bytes(int64_t N, int64_t K, int dtype) {
+  if (N <= 0 || K <= 0 || (dtype != BSG_F16 && dtype != BSG_BF16)) return -1;
+  return cdiv(K, BSG_BLOCK_K) * 64 * cdiv(N, 16) * 16 * 2;
+}
+
+int bsg_pack_weight(const void* w, int64_t N, int64_t K, int64_t stride_n, int64_t stride_k, int dtype,
+                    void* wp, int64_t wp_bytes, void* stream) {
+  if (dtype != BSG_F16 && dtype != BSG_BF16) return fail(BSG_ERR_DTYPE, "dtype=%d", dtype);
+  if (N <= 0 || K <= 0 || stride_n <= 0 || stride_k <= 0)
+    return fail(BSG_ERR_ARG, "pack: N=%lld K=%lld stride_n=%lld stride_k=%lld", (long long)N, (long long)K,
+                (long long)stride_n, (long long)stride_k);
+  if (!w || !wp) return fail(BSG_ERR_ARG, "pack: null pointer");
+  if (!aligned16(wp)) return fail(BSG_ERR_ALIGN, "pack: destination must be 16-byte aligned");
+  if (cdiv(K, BSG_BLOCK_K) > BSG_MAX_NBLK) return fail(BSG_ERR_UNSUPPORTED, "pack: K=%lld too large", (long long)K);
+  const int64_t need = bsg_packed_bytes(N, K, dtype);
+  if (wp_bytes < need) return fail(BSG_ERR_ARG, "pack: destination %lld bytes < %lld", (long long)wp_bytes, (long long)need);
+  const int64_t ntile = cdiv(N, 16);
+  const int64_t groups = cdiv(K, BSG_BLOCK_K) * ntile * 128;
+  const int64_t nb = cdiv(groups, 256);
+  if (nb > 0x7fffffff) return fail(BSG_ERR_UNSUPPORTED, "pack: too large");
+  hipLaunchKernelGGL(bsg_pack_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)w, N, K, stride_n, stride_k, ntile, groups, (uint16_t*)wp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_pack_weight launch");
+  return BSG_OK;
+}
+
+int bsg_plan_resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu_count, bsg_plan* plan) {
+  if (!plan) return fail(BSG_ERR_ARG, "plan is null");
+  return resolve(bt, N, nblk, na, cu_count, plan);
+}
+
+int64_t bsg_gemm_workspace_bytes(int64_t bt, int64_t N, const bsg_plan* plan) {
+  if (!plan || bt <= 0 || N <= 0) return -1;
+  return gemm_ws_bytes(bt, N, plan);
+}
+
+int bsg_workspace_init(void* ws, int64_t ws_bytes, void* stream) {
+  if (ws_bytes < 0 || (ws_bytes > 0 && !ws)) return fail(BSG_ERR_ARG, "workspace_init: bad arguments");
+  if (ws_bytes == 0) return BSG_OK;
+  if (((uintptr_t)ws & 3u) != 0) return fail(BSG_ERR_ALIGN, "workspace must be 4-byte aligned");
+  const int64_t n = ws_bytes / 4;
+  int64_t nb = cdiv(n, 256);
+  if (nb > 4096) nb = 4096;
+  hipLaunchKernelGGL(bsg_zero_kernel, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, (uint32_t*)ws, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_workspace_init launch");
+  return BSG_OK;
+}
+
+int bsg_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+             const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev, void* y,
+             int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, active_blocks, num_active, num_active_dev, nullptr, 0, y,
+                     ldy, dtype, ws, ws_bytes, plan, stream);
+}
+
+int bsg_gemm_bitmap(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+                    const uint8_t* bitmap, int32_t total_k_blocks, void* y, int64_t ldy, int dtype, void* ws,
+                    int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  return launch_gemm(MODE_BITMAP, x, ldx, bt, K, wp, N, nullptr, 0, nullptr, bitmap, total_k_blocks, y, ldy, dtype,
+                     ws, ws_bytes, plan, stream);
+}
+
+int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N, void* y,
+                   int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  return launch_gemm(MODE_DENSE, x, ldx, bt, K, wp, N, nullptr, 0, nullptr, nullptr, 0, y, ldy, dtype, ws,
+                     ws_bytes, plan, stream);
+}
+
+int64_t bsg_select_workspace_bytes(int64_t K) {
+  if (K <= 0) return -1;
+  return cdiv(256 + cdiv(K, BSG_BLOCK_K) * 8, 256) * 256;
+}
+
+int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
+                       int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
+  if (dtype != BSG_F16)
+    return fail(BSG_ERR_DTYPE, "select: exact L1 scoring is defined for fp16 inputs (dtype=%d)", dtype);
+  if (bt <= 0 || K <= 0) return fail(BSG_ERR_ARG, "select: bt=%lld K=%lld", (long long)bt, (long long)K);
+  const int64_t nblk = cdiv(K, BSG_BLOCK_K);
+  if (nblk > BSG_MAX_NBLK) return fail(BSG_ERR_UNSUPPORTED, "select: K=%lld too large", (long long)K);
+  if (k < 0) return fail(BSG_ERR_ARG, "select: k=%d", k);
+  if (!x || !idx_out || !na_out) return fail(BSG_ERR_ARG, "select: null pointer");
+  if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || !aligned16(x))
+    return fail(BSG_ERR_ALIGN, "select: x must be 16-byte aligned, K %% 8 == 0, ldx %% 8 == 0");
+  if (bt * 8 > 0x7fffffff) return fail(BSG_ERR_UNSUPPORTED, "select: bt too large");
+  const int64_t need = bsg_select_workspace_bytes(K);
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
+                (long long)need);
+  SelParams p;
+  p.x = (const uint16_t*)x;
+  p.ldx = ldx;
+  p.cnt = (uint32_t*)ws;
+  p.scores = (uint64_t*)((char*)ws + 256);
+  p.idx_out = idx_out;
+  p.na_out = na_out;
+  p.bt = (int32_t)bt;
+  p.K = (int32_t)K;
+  p.nblk = (int32_t)nblk;
+  p.k = k;
+  hipLaunchKernelGGL(bsg_select_l1_kernel, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 launch");
+  return BSG_OK;
+}
+
+int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp, int64_t N,
+                    int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
+                    const bsg_plan* plan, void* stream) {
+  const int64_t sel = bsg_select_workspace_bytes(K);
+  if (sel < 0) return fail(BSG_ERR_ARG, "select_gemm: K=%lld", (long long)K);
+  int rc = bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
+  if (rc != BSG_OK) return rc;
+  const int64_t nblk = cdiv(K, BSG_BLOCK_K);
+  const int32_t kk = k < nblk ? k : (int32_t)nblk;
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, idx_out, kk, nullptr, nullptr, 0, y, ldy, dtype,
+                     (char*)ws + sel, ws_bytes - sel, plan, stream);
+}
+
+}  // extern "C"
