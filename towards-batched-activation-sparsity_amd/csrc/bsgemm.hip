@@ -69,6 +69,14 @@ __device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
 }
 
+#ifndef BSG_W_AUX
+#define BSG_W_AUX 2  // weight stream: non-temporal (read once, keep X resident in L1/L2)
+#endif
+
+__device__ __forceinline__ u32x4 ld16_stream(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, BSG_W_AUX);
+}
+
 template <typename T>
 struct Elem;
 
@@ -135,18 +143,21 @@ __device__ __forceinline__ void part_store(float* p, float v) {
 #endif
 }
 
-__device__ __forceinline__ f32x4 part_load(const f32x4* p) {
-#if BSG_SPLITK_FENCES
-  return *p;
-#else
-  const float* q = (const float*)p;
+// Components of one fragment lane sit 64 floats apart (see the partial layout).
+__device__ __forceinline__ f32x4 part_load(const float* q) {
   f32x4 v;
+#if BSG_SPLITK_FENCES
+  v.x = q[0];
+  v.y = q[64];
+  v.z = q[128];
+  v.w = q[192];
+#else
   v.x = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.y = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.z = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.w = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
+  v.y = __hip_atomic_load(q + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.z = __hip_atomic_load(q + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.w = __hip_atomic_load(q + 192, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #endif
+  return v;
 }
 
 // Every store of this wave has completed (at the scope it was issued with).
@@ -278,8 +289,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      wd[s][0] = ld16(wr, wcol + s * 2048);
-      wd[s][1] = ld16(wr, wcol + s * 2048 + 1024);
+      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
+      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
     }
     const int kb = (ok ? blk : 0) * 64 + xcol;
 #pragma unroll
@@ -338,16 +349,18 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   };
 
   const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
-  f32x4* part = (f32x4*)p.part;
+  // Partials: [tile][split][fragment][component][lane] floats, so every dword store or load
+  // instruction of a wave covers 256 contiguous bytes.
+  float* const partf = (float*)p.part;
   auto emit = [&](int f, f32x4 v) {
     if (S == 1) {
       store_y(f, v);
     } else {
-      float* dst = (float*)&part[((tile_lin * S + sk) * F + f) * 64 + lane];
+      float* dst = partf + ((tile_lin * S + sk) * F + f) * 256 + lane;
       part_store(dst + 0, v.x);
-      part_store(dst + 1, v.y);
-      part_store(dst + 2, v.z);
-      part_store(dst + 3, v.w);
+      part_store(dst + 64, v.y);
+      part_store(dst + 128, v.z);
+      part_store(dst + 192, v.w);
     }
   };
 
@@ -395,11 +408,36 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
     __syncthreads();
     if (s_misc[WPG]) {
       part_acquire();
-      for (int f = w; f < F; f += WPG) {
-        f32x4 v = part_load(&part[((tile_lin * S) * F + f) * 64 + lane]);
-        for (int q = 1; q < S; ++q) v += part_load(&part[((tile_lin * S + q) * F + f) * 64 + lane]);
-        store_y(f, v);
+      // Work items (fragment, split) of this wave are requested 16 at a time before any is
+      // consumed (one memory round trip per 16), then summed per fragment in split order.
+      const float* base = partf + (tile_lin * S) * F * 256 + lane;
+      constexpr int FW = (F + WPG - 1) / WPG;  // fragments per wave
+      f32x4 acc2[FW];
+#pragma unroll
+      for (int i = 0; i < FW; ++i) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int items = FW * S;
+      for (int i0 = 0; i0 < items; i0 += 16) {
+        f32x4 t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int it = i0 + i;
+          const int fi = it / S, q = it - fi * S, f = w + fi * WPG;
+          if (it < items && f < F) t[i] = part_load(base + ((size_t)q * F + f) * 256);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int it = i0 + i;
+          const int fi = it / S, f = w + fi * WPG;
+          if (it < items && f < F) {
+#pragma unroll
+            for (int j = 0; j < FW; ++j)
+              if (j == fi) acc2[j] += t[i];
+          }
+        }
       }
+#pragma unroll
+      for (int j = 0; j < FW; ++j)
+        if (w + j * WPG < F) store_y(w + j * WPG, acc2[j]);
       if (tid == 0) counter_reset(&p.cnt[tile_lin]);
     }
   }
