@@ -50,11 +50,14 @@ enum bsg_status {
 /* Launch plan of the GEMM.  A zero field means "choose automatically".
  *   split_k         : work-groups that share one output tile and split the active-block
  *                     list (fp32 partials + in-kernel deterministic reduction), >= 1
- *   cols_per_wave   : output columns per wavefront and per work-group: 16, 32, 64 or 128
- *   waves_per_group : wavefronts per work-group; they split the block list and reduce
- *                     through LDS: 1, 2, 4 or 8
+ *   cols_per_wave   : output columns per wavefront: 16, 32, 64 or 128
+ *   waves_per_group : wavefronts per work-group: 1, 2, 4 or 8
  *   depth           : K-blocks whose loads each wave keeps in flight: 1, 2, 4 or 8
  *   rows_per_group  : batch rows per work-group (16, 32 or 64); bt above it adds grid rows
+ *   kind            : 1 = the waves of a work-group split its block list (each loads its own
+ *                     activation fragments); 2 = the waves split the work-group's columns and
+ *                     share each block's activation tile through LDS (work-group columns =
+ *                     cols_per_wave * waves_per_group)
  * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
  * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
 typedef struct bsg_plan {
@@ -63,6 +66,7 @@ typedef struct bsg_plan {
   int32_t waves_per_group;
   int32_t depth;
   int32_t rows_per_group;
+  int32_t kind;
 } bsg_plan;
 
 /* Library identification and thread-local error message. */

@@ -52,26 +52,30 @@ def test_plan_resolve_auto_fills_every_field():
     rc, p = _resolve(16, 4096, 172, 86)
     assert rc == 0
     assert p.split_k >= 1 and p.cols_per_wave in (16, 32, 64, 128) and p.waves_per_group in (1, 2, 4, 8)
-    assert p.depth in (1, 2, 4, 8) and p.rows_per_group == 16
-    assert _resolve(64, 4096, 64, 31)[1].rows_per_group == 64
+    assert p.depth in (1, 2, 4, 8) and p.rows_per_group == 16 and p.kind == 1
+    assert _resolve(64, 4096, 64, 31)[1].rows_per_group == 64 and _resolve(64, 4096, 64, 31)[1].kind == 2
     assert _resolve(2, 4096, 64, 0)[1].split_k == 1
 
 
 def test_plan_resolve_rejects():
     assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(300, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(300, 0, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert "plan" in _lib.last_error()
 
 
 def test_workspace_bytes():
     lib = bsa.load()
-    p = _lib.Plan(1, 32, 4, 4, 16)
+    p = _lib.Plan(1, 32, 4, 4, 16, 1)
     assert lib.bsg_gemm_workspace_bytes(16, 4096, ctypes.byref(p)) == 0
-    p = _lib.Plan(4, 32, 4, 4, 16)
+    p = _lib.Plan(4, 32, 4, 4, 16, 1)
     tiles = 4096 // 32
     assert lib.bsg_gemm_workspace_bytes(16, 4096, ctypes.byref(p)) == 512 + tiles * 4 * 2 * 64 * 16
+    p = _lib.Plan(2, 16, 4, 4, 64, 2)  # kind 2: a work-group covers 16 * 4 columns
+    tiles = 4096 // 64
+    assert lib.bsg_gemm_workspace_bytes(64, 4096, ctypes.byref(p)) == 256 + tiles * 2 * (4 * 4) * 64 * 16
     assert lib.bsg_select_workspace_bytes(4096) == 768
     assert lib.bsg_select_workspace_bytes(0) == -1
 
@@ -81,7 +85,7 @@ FAKE = 1 << 40  # never dereferenced: every call below fails validation first
 
 def test_gemm_rejects_bad_arguments_without_launching():
     lib = bsa.load()
-    p = _lib.Plan(2, 32, 4, 4, 16)
+    p = _lib.Plan(2, 32, 4, 4, 16, 1)
     ok = dict(x=FAKE, ldx=4096, bt=16, K=4096, wp=FAKE, N=4096, idx=FAKE, na=10, nad=None, y=FAKE, ldy=4096,
               dtype=0, ws=FAKE, ws_bytes=1 << 30)
 
@@ -107,7 +111,7 @@ def test_gemm_rejects_bad_arguments_without_launching():
 
 def test_bitmap_and_select_reject_bad_arguments():
     lib = bsa.load()
-    p = _lib.Plan(1, 32, 4, 4, 16)
+    p = _lib.Plan(1, 32, 4, 4, 16, 1)
     assert lib.bsg_gemm_bitmap(FAKE, 4096, 16, 4096, FAKE, 4096, None, 64, FAKE, 4096, 0, None, 0,
                                ctypes.byref(p), None) == _lib.BSG_ERR_ARG
     assert lib.bsg_gemm_bitmap(FAKE, 4096, 16, 4096, FAKE, 4096, FAKE, 65, FAKE, 4096, 0, None, 0,
@@ -133,7 +137,7 @@ def test_status_mapping():
 
 def test_kernel_tiles_and_config_shims():
     tiles = bsa.kernel_tiles()
-    assert (16, 32, 4, 4) in tiles and (64, 64, 4, 2) in tiles
+    assert (1, 16, 32, 4, 4) in tiles and (1, 64, 64, 4, 2) in tiles and (2, 64, 16, 4, 4) in tiles
     from bsa_mi355x import runtime
 
     cfgs = runtime._PREPACK_AUTOTUNE_CONFIGS
@@ -143,6 +147,6 @@ def test_kernel_tiles_and_config_shims():
 
 def test_make_plan_maps_reference_tiles():
     p = bsa.make_plan(4, 16, 64, 2, 3, bt=64)
-    assert p.as_tuple() == (4, 64, 2, 4, 64)   # BLOCK_B raised to cover the batch; stages -> depth 4
-    assert bsa.make_plan().as_tuple() == (0, 0, 0, 0, 0)
+    assert p.as_tuple() == (4, 64, 2, 4, 64, 0)   # BLOCK_B raised to cover the batch; stages -> depth 4
+    assert bsa.make_plan().as_tuple() == (0, 0, 0, 0, 0, 0)
     assert bsa.n_keep_for_density(0.48, 64) == 31

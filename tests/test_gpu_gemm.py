@@ -118,30 +118,30 @@ def test_every_instantiated_tile(dev):
     wb = torch.from_numpy(w_nk.astype(np.float32)).to(torch.bfloat16)
     ref_bf = orc.gemm_ref64(xb.float().numpy(), wb.float().numpy(), idx)
     tiles = bsa.kernel_tiles()
-    assert len(tiles) >= 40
+    assert len(tiles) >= 60
     xt = to_dev(x, dev)
     it = to_dev(idx, dev)
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     packed_b = bsa.pack_weight(wb.to(dev))
-    for rows, cols, waves, depth in tiles:
+    for kind, rows, cols, waves, depth in tiles:
         for sk in (1, 3):
             # explicit plan through gemm_packed, so rows_per_group is honoured even when < bt
             out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
-            p = bsa.Plan(sk, cols, waves, depth, rows)
-            print(f"tile rows={rows} cols={cols} waves={waves} depth={depth} split_k={sk}", flush=True)
+            p = bsa.Plan(sk, cols, waves, depth, rows, kind)
+            print(f"tile kind={kind} rows={rows} cols={cols} waves={waves} depth={depth} split_k={sk}", flush=True)
             bsa.gemm_packed(xt, packed, n, it, out, plan=p, workspace_prefix="tiles")
             torch.cuda.synchronize()
-            assert_close(out.float().cpu().numpy(), ref, f"tile {rows},{cols},{waves},{depth} sk={sk}")
+            assert_close(out.float().cpu().numpy(), ref, f"tile {kind},{rows},{cols},{waves},{depth} sk={sk}")
         # bf16 once per tile (split-K 2)
         out_b = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
-        bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b, plan=bsa.Plan(2, cols, waves, depth, rows),
+        bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b, plan=bsa.Plan(2, cols, waves, depth, rows, kind),
                         workspace_prefix="tiles_bf")
         torch.cuda.synchronize()
         yb = out_b.float().cpu().numpy()
         # bf16 output keeps 8 significant bits: tolerance 5e-3 rel. Frobenius, 2e-2 max-abs
         rf = orc.rel_frobenius(yb, ref_bf)
         assert rf <= 5e-3 and np.max(np.abs(yb - ref_bf)) <= 2e-2 * np.max(np.abs(ref_bf)), \
-            f"bf16 tile {rows},{cols},{waves},{depth}: rel_fro={rf:.3e}"
+            f"bf16 tile {kind},{rows},{cols},{waves},{depth}: rel_fro={rf:.3e}"
 
 
 @pytest.mark.parametrize("split_k", [1, 2, 4, 7, 16, 29])

@@ -57,13 +57,14 @@ class Plan(ctypes.Structure):
         ("waves_per_group", ctypes.c_int32),
         ("depth", ctypes.c_int32),
         ("rows_per_group", ctypes.c_int32),
+        ("kind", ctypes.c_int32),
     ]
 
     def as_tuple(self):
-        return (self.split_k, self.cols_per_wave, self.waves_per_group, self.depth, self.rows_per_group)
+        return (self.split_k, self.cols_per_wave, self.waves_per_group, self.depth, self.rows_per_group, self.kind)
 
     def __repr__(self) -> str:
-        return ("Plan(split_k=%d, cols_per_wave=%d, waves_per_group=%d, depth=%d, rows_per_group=%d)"
+        return ("Plan(split_k=%d, cols_per_wave=%d, waves_per_group=%d, depth=%d, rows_per_group=%d, kind=%d)"
                 % self.as_tuple())
 
 

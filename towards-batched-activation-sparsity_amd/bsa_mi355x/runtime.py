@@ -176,11 +176,11 @@ def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan
     """Resolve a (partial) plan for a problem; tile fields that name a kernel that is not
     instantiated fall back to automatic (the split-K factor is kept)."""
     lib = load()
-    req = Plan(*(plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0)))
+    req = Plan(*(plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0, 0)))
     out = Plan(*req.as_tuple())
     rc = lib.bsg_plan_resolve(bt, n, nblk, na, _cu_count(device), ctypes_byref(out))
     if rc == _lib.BSG_ERR_UNSUPPORTED:
-        out = Plan(req.split_k, 0, 0, 0, 0)
+        out = Plan(req.split_k, 0, 0, 0, 0, 0)
         rc = lib.bsg_plan_resolve(bt, n, nblk, na, _cu_count(device), ctypes_byref(out))
     check(rc)
     return out
@@ -226,19 +226,21 @@ class _KernelHandle:
         p = self.last_plan
         if p is None:
             return None
-        return TileConfig({"BLOCK_B": p.rows_per_group, "BLOCK_N": p.cols_per_wave}, num_warps=p.waves_per_group,
-                          num_stages=p.depth, split_k=p.split_k)
+        cols = p.cols_per_wave * (p.waves_per_group if p.kind == 2 else 1)
+        return TileConfig({"BLOCK_B": p.rows_per_group, "BLOCK_N": cols}, num_warps=p.waves_per_group,
+                          num_stages=p.depth, split_k=p.split_k, kind=p.kind)
 
 
 class TileConfig:
     """Duck-types triton.Config (.kwargs["BLOCK_B"/"BLOCK_N"], .num_warps, .num_stages) for
     the drivers that enumerate tiles (scripts/profile_kernel_configs.py:70-83)."""
 
-    def __init__(self, kwargs: dict, num_warps: int, num_stages: int, split_k: int = 0):
+    def __init__(self, kwargs: dict, num_warps: int, num_stages: int, split_k: int = 0, kind: int = 0):
         self.kwargs = dict(kwargs)
         self.num_warps = int(num_warps)
         self.num_stages = int(num_stages)
         self.split_k = int(split_k)
+        self.kind = int(kind)
 
     def __repr__(self) -> str:
         return (f"TileConfig(BLOCK_B={self.kwargs['BLOCK_B']}, BLOCK_N={self.kwargs['BLOCK_N']}, "
@@ -496,21 +498,23 @@ def dense_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, cache_p
 
 
 def kernel_tiles() -> Sequence[tuple]:
-    """Instantiated (rows_per_group, cols_per_wave, waves_per_group, depth) tuples."""
+    """Instantiated (kind, rows_per_group, cols_per_wave, waves_per_group, depth) tuples."""
     out = []
-    for rows in (16, 32, 64):
-        for cols in (16, 32, 64, 128):
-            for waves in (1, 2, 4, 8):
-                for depth in (1, 2, 4, 8):
-                    p = Plan(1, cols, waves, depth, rows)
-                    if load().bsg_plan_resolve(rows, cols, 1, 1, 1, ctypes_byref(p)) == _lib.BSG_OK:
-                        out.append((rows, cols, waves, depth))
+    for kind in (1, 2):
+        for rows in (16, 32, 64):
+            for cols in (16, 32, 64, 128):
+                for waves in (1, 2, 4, 8):
+                    for depth in (1, 2, 4, 8):
+                        p = Plan(1, cols, waves, depth, rows, kind)
+                        if load().bsg_plan_resolve(rows, cols, 1, 1, 1, ctypes_byref(p)) == _lib.BSG_OK:
+                            out.append((kind, rows, cols, waves, depth))
     return out
 
 
 def __getattr__(name: str):
     if name == "_PREPACK_AUTOTUNE_CONFIGS":
-        cfgs = [TileConfig({"BLOCK_B": r, "BLOCK_N": c}, num_warps=w, num_stages=d) for (r, c, w, d) in kernel_tiles()]
+        cfgs = [TileConfig({"BLOCK_B": r, "BLOCK_N": c * (w if k == 2 else 1)}, num_warps=w, num_stages=d, kind=k)
+                for (k, r, c, w, d) in kernel_tiles()]
         globals()[name] = cfgs
         return cfgs
     raise AttributeError(name)

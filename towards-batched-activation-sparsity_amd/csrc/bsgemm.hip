@@ -197,35 +197,24 @@ struct GemmParams {
   int32_t bt, K, N, npad, nblk, nbm, na, mode, split_k, n_tiles, x_bytes, y_fast;
 };
 
-// One work-group: BTT*16 batch rows x NSUB*16 columns, WPG waves splitting its share of the
-// block list, DEPTH blocks of loads in flight per wave.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
-__global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
-  constexpr int NT = 64 * WPG;
-  constexpr int F = BTT * NSUB;
-  constexpr int RED_BYTES = WPG > 1 ? (WPG - 1) * F * 64 * 16 : 0;  // waves 1..WPG-1
-  constexpr int IDS_BYTES = BSG_MAX_NBLK * 4;
-  // The block list (main loop) and the wave-reduction buffer (epilogue) share LDS.
-  __shared__ __attribute__((aligned(16))) char s_mem[RED_BYTES > IDS_BYTES ? RED_BYTES : IDS_BYTES];
-  __shared__ int s_misc[WPG + 2];
-  int* const s_ids = (int*)s_mem;
-  f32x4* const s_red = (f32x4*)s_mem;
+// ---------------------------------------------------------------------------------------
+// Pieces shared by both GEMM kernel kinds.
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-  // XCD-aware work-group order: hardware places work-group b on XCD b % 8.
+// Work-group -> (column tile, split) with an XCD-aware order: hardware places work-group b
+// on XCD b % 8, so consecutive logical ids (the split partners of a tile) share an XCD.
+__device__ __forceinline__ void tile_of_group(int split_k, int* tile, int* sk) {
   const int nwg = gridDim.x;
   const int bid = blockIdx.x;
   const int lid = (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
-  const int S = p.split_k;
-  const int tile = lid / S;
-  const int sk = lid - tile * S;
-  const int n0 = tile * (16 * NSUB);
-  const int y0 = blockIdx.y * (16 * BTT);
+  *tile = lid / split_k;
+  *sk = lid - *tile * split_k;
+}
 
-  // 1. Stage this call's active-block list in LDS.
+// Stage this call's active-block list in LDS (list copy, bitmap compaction or identity) and
+// return its length.  Ends with a barrier.
+template <int NT>
+__device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
+  const int tid = threadIdx.x;
   int na;
   if (p.mode == MODE_LIST) {
     na = p.na;
@@ -241,7 +230,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
     int c = 0;
     for (int i = beg; i < end; ++i) c += p.bitmap[i] != 0;
     int total = 0;
-    int o = wg_exclusive_scan<NT>(c, s_misc, &total);
+    int o = wg_exclusive_scan<NT>(c, s_scan, &total);
     for (int i = beg; i < end; ++i)
       if (p.bitmap[i] != 0) s_ids[o++] = i;
     na = total;
@@ -251,8 +240,127 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   }
   na = __builtin_amdgcn_readfirstlane(na);
   __syncthreads();
+  return na;
+}
 
-  // 2. This wave's contiguous slice [pbeg, pend) of the list.
+// Output fragment g = bi * CS + cs of a work-group whose columns start at n0 (CS 16-column
+// subtiles): lane holds Y[y0 + 16 bi + lane%16][n0 + 16 cs + 4 (lane/16) + r], r = 0..3.
+template <typename T, int CS>
+__device__ __forceinline__ void store_y(const GemmParams& p, int y0, int n0, int g, f32x4 v) {
+  const int lane = threadIdx.x & 63;
+  const int bi = g / CS;
+  const int cs = g - bi * CS;
+  const int b = y0 + 16 * bi + (lane & 15);
+  const int n = n0 + 16 * cs + 4 * (lane >> 4);
+  if (b >= p.bt) return;
+  uint16_t* yrow = (uint16_t*)p.y + (size_t)b * (size_t)p.ldy;
+  if (p.y_fast) {
+    if (n < p.N) {
+      u32x2 pk;
+      pk.x = (uint32_t)Elem<T>::bits(v.x) | ((uint32_t)Elem<T>::bits(v.y) << 16);
+      pk.y = (uint32_t)Elem<T>::bits(v.z) | ((uint32_t)Elem<T>::bits(v.w) << 16);
+      *(u32x2*)(yrow + n) = pk;
+    }
+  } else {
+    if (n + 0 < p.N) yrow[n + 0] = Elem<T>::bits(v.x);
+    if (n + 1 < p.N) yrow[n + 1] = Elem<T>::bits(v.y);
+    if (n + 2 < p.N) yrow[n + 2] = Elem<T>::bits(v.z);
+    if (n + 3 < p.N) yrow[n + 3] = Elem<T>::bits(v.w);
+  }
+}
+
+// Partials: [tile][split][fragment][component][lane] floats, so every dword store or load
+// instruction of a wave covers 256 contiguous bytes.
+template <int FT>
+__device__ __forceinline__ void part_emit(const GemmParams& p, size_t tile_lin, int sk, int g, f32x4 v) {
+  float* dst = (float*)p.part + ((tile_lin * p.split_k + sk) * FT + g) * 256 + (threadIdx.x & 63);
+  part_store(dst + 0, v.x);
+  part_store(dst + 64, v.y);
+  part_store(dst + 128, v.z);
+  part_store(dst + 192, v.w);
+}
+
+// Split-K hand-off: publish this work-group's partials, count arrivals; the last work-group
+// of the tile reduces the FT fragments in split order and re-arms the counter for the next
+// launch (graph-replay safe).  Partials move through agent-scope (device-coherent) stores and
+// loads, so no L2 write-back/invalidate is needed: each wave waits for its own stores, the
+// barrier orders them before the counter update, and the last work-group loads only after it
+// has seen the final count.
+template <typename T, int FT, int CS, int WPG>
+__device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_lin, int y0, int n0, int w,
+                                              int* s_flag) {
+  const int S = p.split_k;
+  const int lane = threadIdx.x & 63;
+  part_publish();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = counter_add(&p.cnt[tile_lin]);
+    *s_flag = prev == (unsigned)(S - 1);
+  }
+  __syncthreads();
+  if (!*s_flag) return;
+  part_acquire();
+  // Work items (fragment, split) of this wave are requested 16 at a time before any is
+  // consumed (one memory round trip per 16), then summed per fragment in split order.
+  const float* base = (const float*)p.part + (tile_lin * S) * FT * 256 + lane;
+  constexpr int FW = (FT + WPG - 1) / WPG;  // fragments per wave
+  f32x4 acc2[FW];
+#pragma unroll
+  for (int i = 0; i < FW; ++i) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int items = FW * S;
+  for (int i0 = 0; i0 < items; i0 += 16) {
+    f32x4 t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int it = i0 + i;
+      const int fi = it / S, q = it - fi * S, g = w + fi * WPG;
+      if (it < items && g < FT) t[i] = part_load(base + ((size_t)q * FT + g) * 256);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int it = i0 + i;
+      const int fi = it / S, g = w + fi * WPG;
+      if (it < items && g < FT) {
+#pragma unroll
+        for (int j = 0; j < FW; ++j)
+          if (j == fi) acc2[j] += t[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < FW; ++j)
+    if (w + j * WPG < FT) store_y<T, CS>(p, y0, n0, w + j * WPG, acc2[j]);
+  if (threadIdx.x == 0) counter_reset(&p.cnt[tile_lin]);
+}
+
+// ---------------------------------------------------------------------------------------
+// Kind 1 ("ksplit"): one work-group = BTT*16 batch rows x NSUB*16 columns; its WPG waves split
+// the work-group's share of the block list into contiguous slices and are reduced through LDS
+// in wave order.  Each wave loads its own X fragments.  Best when bt is small (the X fragments
+// are few) and many narrow column tiles are needed to fill the chip.
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
+__global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
+  constexpr int NT = 64 * WPG;
+  constexpr int F = BTT * NSUB;
+  constexpr int RED_BYTES = WPG > 1 ? (WPG - 1) * F * 64 * 16 : 0;  // waves 1..WPG-1
+  constexpr int IDS_BYTES = BSG_MAX_NBLK * 4;
+  // The block list (main loop) and the wave-reduction buffer (epilogue) share LDS.
+  __shared__ __attribute__((aligned(16))) char s_mem[RED_BYTES > IDS_BYTES ? RED_BYTES : IDS_BYTES];
+  __shared__ int s_misc[WPG + 2];
+  int* const s_ids = (int*)s_mem;
+  f32x4* const s_red = (f32x4*)s_mem;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tile, sk;
+  tile_of_group(p.split_k, &tile, &sk);
+  const int S = p.split_k;
+  const int n0 = tile * (16 * NSUB);
+  const int y0 = blockIdx.y * (16 * BTT);
+
+  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+
+  // This wave's contiguous slice [pbeg, pend) of the list.
   const int G = S * WPG;
   const int g = sk * WPG + w;
   const int pbeg = (int)(((int64_t)na * g) / G);
@@ -313,8 +421,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
         for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][h], xd[bi][h], acc[bi][s]);
   };
 
-  // 3. Rolling pipeline: DEPTH blocks in flight; loads past the slice are out-of-range
-  //    (zero, no memory traffic) so the body has no data-dependent branches.
+  // Rolling pipeline: DEPTH blocks in flight; loads past the slice are out-of-range (zero,
+  // no memory traffic) so the body has no data-dependent branches.
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
   for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
@@ -325,43 +433,12 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
     }
   }
 
-  // 4. Output.  Fragment f = (bi, s): lane holds Y[y0+16bi+lane%16][n0+16s+4(lane/16)+r].
-  auto store_y = [&](int f, f32x4 v) {
-    const int bi = f / NSUB;
-    const int s = f - bi * NSUB;
-    const int b = y0 + 16 * bi + (lane & 15);
-    const int n = n0 + 16 * s + 4 * (lane >> 4);
-    if (b >= p.bt) return;
-    uint16_t* yrow = (uint16_t*)p.y + (size_t)b * (size_t)p.ldy;
-    if (p.y_fast) {
-      if (n < p.N) {
-        u32x2 pk;
-        pk.x = (uint32_t)Elem<T>::bits(v.x) | ((uint32_t)Elem<T>::bits(v.y) << 16);
-        pk.y = (uint32_t)Elem<T>::bits(v.z) | ((uint32_t)Elem<T>::bits(v.w) << 16);
-        *(u32x2*)(yrow + n) = pk;
-      }
-    } else {
-      if (n + 0 < p.N) yrow[n + 0] = Elem<T>::bits(v.x);
-      if (n + 1 < p.N) yrow[n + 1] = Elem<T>::bits(v.y);
-      if (n + 2 < p.N) yrow[n + 2] = Elem<T>::bits(v.z);
-      if (n + 3 < p.N) yrow[n + 3] = Elem<T>::bits(v.w);
-    }
-  };
-
   const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
-  // Partials: [tile][split][fragment][component][lane] floats, so every dword store or load
-  // instruction of a wave covers 256 contiguous bytes.
-  float* const partf = (float*)p.part;
   auto emit = [&](int f, f32x4 v) {
-    if (S == 1) {
-      store_y(f, v);
-    } else {
-      float* dst = partf + ((tile_lin * S + sk) * F + f) * 256 + lane;
-      part_store(dst + 0, v.x);
-      part_store(dst + 64, v.y);
-      part_store(dst + 128, v.z);
-      part_store(dst + 192, v.w);
-    }
+    if (S == 1)
+      store_y<T, NSUB>(p, y0, n0, f, v);
+    else
+      part_emit<F>(p, tile_lin, sk, f, v);
   };
 
   if constexpr (WPG > 1) {
@@ -392,55 +469,122 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
   }
 
-  if (S > 1) {
-    // Publish the partial, count arrivals; the last work-group of the tile reduces in
-    // split order and re-arms the counter for the next launch (graph-replay safe).
-    // Partials move through agent-scope (device-coherent) stores and loads, so no L2
-    // write-back/invalidate is needed: each wave waits for its own stores to complete,
-    // the barrier orders them before the counter update, and the last work-group issues
-    // its loads only after it has seen the final count.
-    part_publish();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = counter_add(&p.cnt[tile_lin]);
-      s_misc[WPG] = prev == (unsigned)(S - 1);
+  if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
+}
+
+// Kind 2 ("xlds"): one work-group = BTT*16 batch rows x WPG*NSUB*16 columns; its waves split
+// the columns and walk the same block list together.  Each block's X tile (BTT*16 rows x 64
+// channels) is loaded once per work-group, in MFMA B-fragment order, into a double-buffered
+// LDS stage (one barrier per block) and shared by every wave, so X costs 1/WPG of the loads
+// of kind 1 and the prefetch registers hold weights only.  Best for larger batches.
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
+__global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
+  constexpr int NT = 64 * WPG;
+  constexpr int XF = 2 * BTT;                // X fragments (1 KiB each) per block
+  constexpr int XPW = (XF + WPG - 1) / WPG;  // X fragments each wave loads per block
+  constexpr int CS = WPG * NSUB;             // 16-column subtiles per work-group
+  constexpr int FT = BTT * CS;               // output fragments per work-group
+  __shared__ int s_ids[BSG_MAX_NBLK];
+  __shared__ __attribute__((aligned(16))) u32x4 s_x[2][XF][64];
+  __shared__ int s_misc[WPG + 2];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tile, sk;
+  tile_of_group(p.split_k, &tile, &sk);
+  const int S = p.split_k;
+  const int n0 = tile * (16 * CS);
+  const int y0 = blockIdx.y * (16 * BTT);
+
+  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+
+  // The work-group's contiguous slice of the list (all its waves walk it together).
+  const int pbeg = (int)(((int64_t)na * sk) / S);
+  const int pend = (int)(((int64_t)na * (sk + 1)) / S);
+  const int cnt = pend - pbeg;
+
+  const int blk_bytes = p.npad * 128;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  // X fragments this wave brings in: f = w + j*WPG -> batch tile f/2, k-half f%2.
+  int xrow_off[XPW];
+  bool xrow_ok[XPW];
+  int xcol[XPW];
+#pragma unroll
+  for (int j = 0; j < XPW; ++j) {
+    const int f = w + j * WPG;
+    const int row = y0 + 16 * (f >> 1) + (lane & 15);
+    xrow_ok[j] = f < XF && row < p.bt;
+    xrow_off[j] = xrow_ok[j] ? row * (int)p.ldx * 2 : 0;
+    xcol[j] = 32 * (f & 1) + 8 * (lane >> 4);
+  }
+  const int wcol = lane * 16 + ((n0 >> 4) + w * NSUB) * 2048;
+
+  u32x4 wv[DEPTH][NSUB][2];
+  u32x4 xs[DEPTH][XPW];
+  f32x4 acc[BTT][NSUB];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](u32x4 (&wd)[NSUB][2], u32x4 (&xd)[XPW], int t) {
+    const int q = t < cnt ? pbeg + t : 0;
+    int blk = s_ids[q];
+    blk = __builtin_amdgcn_readfirstlane(blk);
+    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
+      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
     }
-    __syncthreads();
-    if (s_misc[WPG]) {
-      part_acquire();
-      // Work items (fragment, split) of this wave are requested 16 at a time before any is
-      // consumed (one memory round trip per 16), then summed per fragment in split order.
-      const float* base = partf + (tile_lin * S) * F * 256 + lane;
-      constexpr int FW = (F + WPG - 1) / WPG;  // fragments per wave
-      f32x4 acc2[FW];
+    const int kb = (ok ? blk : 0) * 64;
 #pragma unroll
-      for (int i = 0; i < FW; ++i) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int items = FW * S;
-      for (int i0 = 0; i0 < items; i0 += 16) {
-        f32x4 t[16];
+    for (int j = 0; j < XPW; ++j) {
+      const int col = kb + xcol[j];
+      const bool v = ok && xrow_ok[j] && col < p.K;
+      xd[j] = ld16(xr, v ? xrow_off[j] + col * 2 : kOOB);
+    }
+  };
+
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int it = i0 + i;
-          const int fi = it / S, q = it - fi * S, f = w + fi * WPG;
-          if (it < items && f < F) t[i] = part_load(base + ((size_t)q * F + f) * 256);
-        }
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xs[d], d);
+  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int it = i0 + i;
-          const int fi = it / S, f = w + fi * WPG;
-          if (it < items && f < F) {
+    for (int d = 0; d < DEPTH; ++d) {
+      const int stage = (t0 + d) & 1;
+      // Publish X of block t0+d; after the barrier every wave has also finished reading the
+      // stage it will overwrite next iteration.
 #pragma unroll
-            for (int j = 0; j < FW; ++j)
-              if (j == fi) acc2[j] += t[i];
-          }
+      for (int j = 0; j < XPW; ++j)
+        if (w + j * WPG < XF) s_x[stage][w + j * WPG][lane] = xs[d][j];
+      __syncthreads();
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int bi = 0; bi < BTT; ++bi) {
+          const u32x4 xb = s_x[stage][2 * bi + h][lane];
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][h], xb, acc[bi][s]);
         }
       }
-#pragma unroll
-      for (int j = 0; j < FW; ++j)
-        if (w + j * WPG < F) store_y(w + j * WPG, acc2[j]);
-      if (tid == 0) counter_reset(&p.cnt[tile_lin]);
+      issue(wv[d], xs[d], t0 + d + DEPTH);
     }
   }
+
+  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      const int g = bi * CS + w * NSUB + s;
+      if (S == 1)
+        store_y<T, CS>(p, y0, n0, g, acc[bi][s]);
+      else
+        part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
+    }
+  if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
 }
 
 // Pack W (logical [N,K], element strides sn/sk) into the tiled K-major layout.
@@ -564,17 +708,22 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
 
 typedef void (*GemmFn)(GemmParams);
 
+enum { KIND_KSPLIT = 1, KIND_XLDS = 2 };
+
 struct KernelEntry {
-  int btt, nsub, wpg, depth;
+  int kind, btt, nsub, wpg, depth;
   GemmFn f16, bf16;
 };
 
 #define BSG_K(B, S, W, D) \
-  {B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
+  {KIND_KSPLIT, B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
+#define BSG_X(B, S, W, D) \
+  {KIND_XLDS, B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, D>}
 
-// Instantiated tile set.  Register budget per lane ~ depth*(nsub+btt)*8 + btt*nsub*4.
+// Instantiated tile set.  Kind 1 registers per lane ~ depth*(nsub+btt)*8 + btt*nsub*4;
+// kind 2 ~ depth*(nsub*8 + ceil(2*btt/wpg)*4) + btt*nsub*4.
 const KernelEntry kKernels[] = {
-    // 16 batch rows
+    // kind 1, 16 batch rows
     BSG_K(1, 1, 1, 4), BSG_K(1, 1, 1, 8), BSG_K(1, 1, 2, 4), BSG_K(1, 1, 2, 8),
     BSG_K(1, 1, 4, 2), BSG_K(1, 1, 4, 4), BSG_K(1, 1, 4, 8), BSG_K(1, 1, 8, 2),
     BSG_K(1, 1, 8, 4), BSG_K(1, 1, 8, 8),
@@ -584,26 +733,38 @@ const KernelEntry kKernels[] = {
     BSG_K(1, 4, 1, 4), BSG_K(1, 4, 2, 4), BSG_K(1, 4, 4, 2), BSG_K(1, 4, 4, 4),
     BSG_K(1, 4, 8, 2),
     BSG_K(1, 8, 1, 2), BSG_K(1, 8, 2, 2), BSG_K(1, 8, 4, 2),
-    // 32 batch rows
+    // kind 1, 32 batch rows
     BSG_K(2, 2, 1, 4), BSG_K(2, 2, 2, 4), BSG_K(2, 2, 4, 2), BSG_K(2, 2, 4, 4),
     BSG_K(2, 4, 1, 4), BSG_K(2, 4, 2, 2), BSG_K(2, 4, 2, 4), BSG_K(2, 4, 4, 2),
-    // 64 batch rows
+    // kind 1, 64 batch rows
     BSG_K(4, 2, 1, 4), BSG_K(4, 2, 2, 2), BSG_K(4, 2, 2, 4), BSG_K(4, 2, 4, 2),
     BSG_K(4, 4, 1, 2), BSG_K(4, 4, 1, 4), BSG_K(4, 4, 2, 2), BSG_K(4, 4, 4, 1),
     BSG_K(4, 4, 4, 2),
     BSG_K(4, 8, 1, 2), BSG_K(4, 8, 2, 1), BSG_K(4, 8, 2, 2),
+    // kind 2 (X staged in LDS, waves split columns)
+    BSG_X(1, 1, 2, 4), BSG_X(1, 1, 4, 4), BSG_X(1, 1, 4, 8), BSG_X(1, 1, 8, 4), BSG_X(1, 2, 2, 4),
+    BSG_X(1, 2, 4, 4),
+    BSG_X(2, 1, 2, 4), BSG_X(2, 1, 4, 4), BSG_X(2, 1, 4, 8), BSG_X(2, 2, 2, 4), BSG_X(2, 2, 4, 4),
+    BSG_X(4, 1, 2, 4), BSG_X(4, 1, 4, 4), BSG_X(4, 1, 4, 8), BSG_X(4, 1, 8, 4), BSG_X(4, 2, 2, 2),
+    BSG_X(4, 2, 2, 4), BSG_X(4, 2, 4, 2), BSG_X(4, 2, 4, 4), BSG_X(4, 4, 2, 2), BSG_X(4, 4, 4, 2),
 };
 #undef BSG_K
+#undef BSG_X
 
-const KernelEntry* find_kernel(int btt, int nsub, int wpg, int depth) {
+const KernelEntry* find_kernel(int kind, int btt, int nsub, int wpg, int depth) {
   for (const KernelEntry& e : kKernels)
-    if (e.btt == btt && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
+    if (e.kind == kind && e.btt == btt && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
   return nullptr;
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
+
+// Columns covered by one work-group of a resolved plan.
+int64_t group_cols(const bsg_plan* pl) {
+  return (int64_t)pl->cols_per_wave * (pl->kind == KIND_XLDS ? pl->waves_per_group : 1);
+}
 
 int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_plan* pl) {
   if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
@@ -613,22 +774,32 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
   const int rpg = pl->rows_per_group;
   if (rpg != 16 && rpg != 32 && rpg != 64)
     return fail(BSG_ERR_UNSUPPORTED, "plan: rows_per_group=%d (16, 32 or 64)", rpg);
+  if (pl->kind == 0) pl->kind = rpg == 16 ? KIND_KSPLIT : KIND_XLDS;
+  if (pl->kind != KIND_KSPLIT && pl->kind != KIND_XLDS)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X in LDS)", pl->kind);
   const int auto_fields = (pl->cols_per_wave == 0 ? 1 : 0) | (pl->waves_per_group == 0 ? 2 : 0) |
                           (pl->depth == 0 ? 4 : 0);
-  if (pl->cols_per_wave == 0) pl->cols_per_wave = rpg == 16 ? 32 : 64;
-  if (pl->waves_per_group == 0) pl->waves_per_group = 4;
-  if (pl->depth == 0) pl->depth = rpg == 64 ? 2 : 4;
+  if (pl->kind == KIND_KSPLIT) {
+    if (pl->cols_per_wave == 0) pl->cols_per_wave = rpg == 16 ? 16 : 32;
+    if (pl->waves_per_group == 0) pl->waves_per_group = rpg == 16 ? 2 : 4;
+    if (pl->depth == 0) pl->depth = rpg == 64 ? 2 : 4;
+  } else {
+    if (pl->cols_per_wave == 0) pl->cols_per_wave = 16;
+    if (pl->waves_per_group == 0) pl->waves_per_group = 4;
+    if (pl->depth == 0) pl->depth = 4;
+  }
   if (!pow2_in(pl->cols_per_wave, 16, 128) || !pow2_in(pl->waves_per_group, 1, 8) ||
       !pow2_in(pl->depth, 1, 8))
     return fail(BSG_ERR_UNSUPPORTED, "plan: cols_per_wave=%d waves_per_group=%d depth=%d",
                 pl->cols_per_wave, pl->waves_per_group, pl->depth);
-  if (!find_kernel(rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth) && auto_fields) {
+  if (!find_kernel(pl->kind, rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth) &&
+      auto_fields) {
     // An automatic field led to a tile that is not compiled: take the instantiated kernel
     // that keeps every explicit field and is closest in the automatic ones.
     const KernelEntry* best = nullptr;
     int best_d = 1 << 30;
     for (const KernelEntry& e : kKernels) {
-      if (e.btt != rpg / 16) continue;
+      if (e.kind != pl->kind || e.btt != rpg / 16) continue;
       if (!(auto_fields & 1) && e.nsub * 16 != pl->cols_per_wave) continue;
       if (!(auto_fields & 2) && e.wpg != pl->waves_per_group) continue;
       if (!(auto_fields & 4) && e.depth != pl->depth) continue;
@@ -645,17 +816,19 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
       pl->depth = best->depth;
     }
   }
-  if (!find_kernel(rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
+  if (!find_kernel(pl->kind, rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
     return fail(BSG_ERR_UNSUPPORTED,
-                "plan: no kernel instantiated for rows_per_group=%d cols_per_wave=%d "
+                "plan: no kernel instantiated for kind=%d rows_per_group=%d cols_per_wave=%d "
                 "waves_per_group=%d depth=%d",
-                rpg, pl->cols_per_wave, pl->waves_per_group, pl->depth);
+                pl->kind, rpg, pl->cols_per_wave, pl->waves_per_group, pl->depth);
   if (pl->split_k == 0) {
-    const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, pl->cols_per_wave);
+    // Enough work-groups to cover every compute unit once, without giving a wave fewer than
+    // two blocks; kind 1 also counts its waves as list splitters.
+    const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, group_cols(pl));
     const int64_t groups = n_tiles * cdiv(bt, rpg);
-    const int64_t target = (int64_t)cu * 8;  // waves
-    int64_t s = cdiv(target, groups * pl->waves_per_group);
-    const int64_t by_work = (int64_t)na / (2 * pl->waves_per_group);  // >= 2 blocks per wave
+    int64_t s = cdiv(cu, groups);
+    const int64_t splitters = pl->kind == KIND_KSPLIT ? pl->waves_per_group : 1;
+    const int64_t by_work = (int64_t)na / (2 * splitters);
     if (s > by_work) s = by_work;
     if (s > 32) s = 32;
     if (s < 1) s = 1;
@@ -668,9 +841,9 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
 
 int64_t gemm_ws_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
   if (pl->split_k <= 1) return 0;
-  const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, pl->cols_per_wave);
+  const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, group_cols(pl));
   const int64_t tiles = n_tiles * cdiv(bt, pl->rows_per_group);
-  const int64_t frag = (int64_t)(pl->rows_per_group / 16) * (pl->cols_per_wave / 16);
+  const int64_t frag = (int64_t)(pl->rows_per_group / 16) * (group_cols(pl) / 16);
   const int64_t part = tiles * pl->split_k * frag * 64 * 16;
   const int64_t counters = cdiv(tiles * 4, 256) * 256;
   return counters + part;
@@ -729,7 +902,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   } else {
     na = nblk;
   }
-  bsg_plan pl = plan_in ? *plan_in : bsg_plan{0, 0, 0, 0, 0};
+  bsg_plan pl = plan_in ? *plan_in : bsg_plan{0, 0, 0, 0, 0, 0};
   int cu = 256;
   if (pl.split_k == 0) cu = device_cu_count();  // only feeds the automatic split-K choice
   rc = resolve(bt, N, nblk, na, cu, &pl);
@@ -739,9 +912,10 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(BSG_ERR_WORKSPACE, "workspace %lld bytes < %lld needed (split_k=%d)", (long long)ws_bytes,
                 (long long)need, pl.split_k);
-  const KernelEntry* ke = find_kernel(pl.rows_per_group / 16, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
+  const KernelEntry* ke =
+      find_kernel(pl.kind, pl.rows_per_group / 16, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
   const int64_t npad = cdiv(N, 16) * 16;
-  const int64_t n_tiles = cdiv(npad, pl.cols_per_wave);
+  const int64_t n_tiles = cdiv(npad, group_cols(&pl));
   const int64_t ygroups = cdiv(bt, pl.rows_per_group);
   if (n_tiles * pl.split_k > 0x7fffffff || ygroups > 65535) return fail(BSG_ERR_UNSUPPORTED, "grid too large");
 
