@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 1 << 30
 METRIC = "µs/GEMM + HBM GB/s + speedup vs dense, Llama-2-7B shapes at B=2/16/64"
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_down_b16_s050.json")
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md")
 
 
 def log(msg: str) -> None:
@@ -50,6 +50,9 @@ def parse_args():
     ap.add_argument("--workload", default="down_sweep", choices=["down_sweep", "llama", "fused"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default=None, help="time only this point (profiling runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the GEMMs, replay a plain device copy of MIB MiB (PMC calibration)")
     return ap.parse_args()
 
 
@@ -76,7 +79,7 @@ class Point:
         self.packed = [packed] + [packed.clone() for _ in range(self.copies - 1)]
         self.idx = torch.from_numpy(idx).to(dev)
         self.y = torch.empty(bt, n, dtype=torch.float16, device=dev)
-        self.plan = bsa.resolve_plan(bt, n, nb, nb if dense else na, dev, plan)
+        self.plan = bsa.resolve_plan(bt, n, nb, nb if dense else na, dev, plan, dense=dense)
         self.active_bytes = (nb if dense else na) * 64 * n * 2
         self.flops = 2 * bt * (nb if dense else na) * 64 * n
         self.graph = None
@@ -188,11 +191,62 @@ def cpu_baseline(point, seconds):
 
 
 def load_traffic():
+    """HBM bytes per launch of the roofline point, from the committed PMC summary (a line
+    `traffic_bytes_per_launch: <int>`), or None when no summary is present."""
     try:
         with open(PROFILE_TRAFFIC) as f:
-            return json.load(f).get("bytes_per_launch")
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
     except (OSError, ValueError):
-        return None
+        pass
+    return None
+
+
+def copy_calibration(mib, steps):
+    """Replay a plain device-to-device copy of `mib` MiB (known bytes) for PMC scaling."""
+    import torch
+
+    n = mib * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    g = torch.cuda.CUDAGraph()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        dst.copy_(src)
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 2, "bytes_written": n * 2, "launches": steps + 1}))
+
+
+def torch_mm_us(point, reps=5):
+    """hipBLASLt dense GEMM (torch.mm) on the same shape, rotated over weight copies: context."""
+    import torch
+
+    w0 = torch.from_numpy(point.w_kn_np).to(point.x.device)
+    ws = [w0] + [w0.clone() for _ in range(point.copies - 1)]
+    out = torch.empty(point.bt, point.n, dtype=torch.float16, device=point.x.device)
+    torch.mm(point.x, ws[0], out=out)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for w in ws:
+            torch.mm(point.x, w, out=out)
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b) * 1000.0 / len(ws))
+    del g, ws
+    return statistics.median(ts)
 
 
 def main():
@@ -208,6 +262,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, args.steps)
+        return
     bsa.load()
     log(f"device {torch.cuda.get_device_name(dev)}; lib {bsa.load().bsg_version().decode()}")
 
@@ -237,6 +294,11 @@ def main():
     else:
         raise SystemExit("workload 'fused' is measured by tests and DESIGN notes; not a bench line yet")
 
+    if args.only:
+        points = [p for p in points if p.name == args.only]
+        if not points:
+            raise SystemExit(f"--only {args.only}: no such point")
+        focus = points[0].name
     bad = []
     for p in points:
         rf, ok = p.check()
@@ -285,8 +347,15 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                 "kernel": "bsg_gemm_kernel", "point": focus, "avg_launch_us": round(f_mean, 3),
                 "bytes_per_launch": fp.active_bytes}
+    dense_pt = next((p for p in points if p.dense and p.name.startswith("down_b16")), None)
+    if dense_pt is not None and not args.only:
+        mm = torch_mm_us(dense_pt)
+        for row in out_points:
+            if row["name"] == dense_pt.name:
+                row["torch_mm_us"] = round(mm, 3)
+        log(f"torch.mm (hipBLASLt) on {dense_pt.name}: {mm:.2f} us")
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.only:
         log("cpu baseline ...")
         cpu = cpu_baseline(fp, args.cpu_seconds)
     line = {

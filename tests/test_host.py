@@ -1,0 +1,94 @@
+"""Host-side logic without a GPU: tuned-plan lookup, the reference's lookup-table schemas,
+reference tile -> plan mapping, and the drop-in module path."""
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+
+import bsa_mi355x as bsa
+from bsa_mi355x import tuning
+
+
+def test_shipped_table_covers_baseline_shapes():
+    entries = tuning.load_table()
+    assert entries, "tuned_plans.json missing or empty"
+    shapes = {(e["N"], e["K"]) for e in entries}
+    assert {(4096, 4096), (11008, 4096), (4096, 11008)} <= shapes
+    assert {e["bt"] for e in entries} >= {2, 16, 64}
+    assert any(e["dense"] for e in entries)
+    for e in entries:
+        assert len(e["plan"]) == 6 and e["plan"][0] >= 1 and e["plan"][5] in (1, 2)
+
+
+def test_lookup_nearest_batch_and_density():
+    tuning.load_table()
+    p = tuning.lookup(16, 4096, 172, 86)
+    assert p is not None and p.rows_per_group == 16
+    assert tuning.lookup(64, 11008, 64, 31).rows_per_group == 64
+    assert tuning.lookup(8, 4096, 172, 80) is not None        # nearest batch in the 16-row bucket
+    assert tuning.lookup(16, 1234, 172, 86) is None           # shape not tabulated
+    d = tuning.lookup(16, 4096, 172, 172, dense=True)
+    assert d is not None
+
+
+def test_lookup_from_custom_table(tmp_path):
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"entries": [
+        {"bt": 16, "N": 100, "K": 640, "na": 3, "dense": False, "plan": [2, 16, 4, 4, 16, 1], "us": 1.0},
+        {"bt": 16, "N": 100, "K": 640, "na": 8, "dense": False, "plan": [1, 32, 2, 4, 16, 1], "us": 1.0},
+    ]}))
+    tuning.load_table(str(path))
+    try:
+        assert tuning.lookup(16, 100, 10, 4).as_tuple() == (2, 16, 4, 4, 16, 1)
+        assert tuning.lookup(16, 100, 10, 7).as_tuple() == (1, 32, 2, 4, 16, 1)
+        assert tuning.lookup(64, 100, 10, 7) is None          # no 64-row entry
+    finally:
+        tuning.load_table()
+
+
+def test_reference_lookup_both_key_sets(tmp_path):
+    pkc = {"down": {"0.5": {"mask": "bitmap", "block_k": 64, "K": 4, "tile": [16, 64, 2, 3],
+                            "dense_ms": 0.05, "sparse_ms": 0.03, "speedup": 1.6},
+                    "1.0": {"mask": "dense", "K": 1, "tile": None}}}
+    rrd = {"down": {"0.5": {"best_kern": "naive", "best_K": 2, "best_tile": [32, 128, 4, 2]}}}
+    p1 = tmp_path / "llama2_kernel_best_sweep_B16.json"
+    p1.write_text(json.dumps(pkc))
+    p2 = tmp_path / "rrd.json"
+    p2.write_text(json.dumps(rrd))
+    a = tuning.load_reference_lookup(str(p1))
+    b = tuning.load_reference_lookup(str(p2))
+    key, cfg = tuning.nearest_density_cfg(a["down"], 0.47)
+    assert key == 0.5 and cfg["mask"] == "bitmap"
+    assert tuning.plan_from_reference_cfg(cfg, bt=16).as_tuple() == (4, 64, 2, 4, 16, 0)
+    assert tuning.plan_from_reference_cfg(a["down"][1.0], bt=16) is None
+    cfg_b = b["down"][0.5]
+    assert cfg_b["mask"] == "naive" and cfg_b["K"] == 2
+    assert tuning.plan_from_reference_cfg(cfg_b, bt=16).as_tuple() == (2, 128, 4, 2, 32, 0)
+    own = {"plan": [3, 16, 4, 4, 64, 2], "mask": "naive", "K": 3}
+    assert tuning.plan_from_reference_cfg(own, bt=64).as_tuple() == (3, 16, 4, 4, 64, 2)
+
+
+def test_dropin_module_path_exports_reference_names():
+    from kernels.shared_mask_batched_triton_min_runtime import (  # noqa: F401
+        INDEX_BLOCK_META_SIZE, _PREPACK_AUTOTUNE_CONFIGS, _build_active_k_bitmap, _get_prepacked_weight_block_major,
+        _prepacked_block_sparse_gemm_from_active_blocks,
+        _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload,
+        _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload_splitk,
+        _prepacked_block_sparse_gemm_from_active_blocks_splitk, prepacked_block_sparse_gemm_batched_kernel,
+        prepacked_block_sparse_gemm_bitmap_preload_batched_kernel)
+    assert INDEX_BLOCK_META_SIZE == 64
+    assert prepacked_block_sparse_gemm_bitmap_preload_batched_kernel.best_config is None
+    cfg = _PREPACK_AUTOTUNE_CONFIGS[0]
+    assert cfg.kwargs["BLOCK_B"] in (16, 32, 64) and cfg.num_warps in (1, 2, 4, 8)
+
+
+def test_cpu_tensors_are_rejected():
+    import torch
+
+    x = torch.zeros(2, 1, 64, dtype=torch.float16)
+    w = torch.zeros(16, 64, dtype=torch.float16)
+    out = torch.zeros(2, 1, 16, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(x, w, torch.tensor([0], dtype=torch.int32), out)

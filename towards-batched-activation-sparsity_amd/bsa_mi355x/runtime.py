@@ -172,10 +172,19 @@ def make_plan(num_split_k: Optional[int] = None, tile_b: Optional[int] = None, t
     return p
 
 
-def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan: Optional[Plan] = None) -> Plan:
-    """Resolve a (partial) plan for a problem; tile fields that name a kernel that is not
-    instantiated fall back to automatic (the split-K factor is kept)."""
+def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan: Optional[Plan] = None,
+                 dense: bool = False, lookup_plan: bool = True) -> Plan:
+    """Resolve a (partial) plan for a problem.  With no plan (or an all-zero one) the tuned
+    table (tuning.lookup) is consulted first; remaining zero fields are filled by the library's
+    heuristics; tile fields that name a kernel that is not instantiated fall back to automatic
+    (the split-K factor is kept)."""
     lib = load()
+    if lookup_plan and (plan is None or not any(plan.as_tuple())):
+        from . import tuning
+
+        tuned = tuning.lookup(bt, n, nblk, na, dense=dense)
+        if tuned is not None:
+            plan = tuned
     req = Plan(*(plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0, 0)))
     out = Plan(*req.as_tuple())
     rc = lib.bsg_plan_resolve(bt, n, nblk, na, _cu_count(device), ctypes_byref(out))
@@ -322,7 +331,7 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
     else:
         mode = "dense"
         na_for_plan = nblk
-    pl = resolve_plan(bt, n_dim, nblk, na_for_plan, dev, plan)
+    pl = resolve_plan(bt, n_dim, nblk, na_for_plan, dev, plan, dense=(mode == "dense"))
     ws_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
     ws_ptr = _workspace(workspace_prefix, dev, ws_bytes).data_ptr() if ws_bytes > 0 else None
     kd = x2d.shape[1]
