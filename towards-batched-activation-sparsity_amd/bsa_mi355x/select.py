@@ -72,15 +72,26 @@ def select_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
 
     x [B, S, K], weight nn.Linear [N, K], out [B, S, N].  Two launches on the current stream,
     no host round trip; returns the (device) selected list and count."""
-    lib = load()
     n_dim = out.shape[-1]
     x2d, y2d, bt, m_dim = _views(x, out, n_dim)
     _check_shapes(x2d, weight, y2d, n_dim, m_dim)
-    if m_dim % 8 != 0:
-        raise ValueError(f"K={m_dim} must be a multiple of 8 for the fused selector")
-    dev = _require_cuda(x2d, weight, y2d)
     entry = _packed_entry(weight, BLOCK_K, cache_prefix)
-    nblk = entry.nblk
+    return select_gemm_packed(x2d, entry.packed, n_dim, k, y2d, plan=plan, idx_out=idx_out, count_out=count_out,
+                              workspace_prefix=f"{cache_prefix}_ws")
+
+
+def select_gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor, plan=None,
+                       idx_out: Optional[torch.Tensor] = None, count_out: Optional[torch.Tensor] = None,
+                       workspace_prefix: str = "sel_gemm_ws") -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fused selection + GEMM on an already packed weight: x2d [bt, K] fp16, y2d [bt, N]."""
+    lib = load()
+    dev = _require_cuda(x2d, packed, y2d)
+    bt, m_dim = x2d.shape
+    if m_dim % 8 != 0 or x2d.stride(1) != 1 or x2d.stride(0) % 8 != 0:
+        raise ValueError(f"x must be [bt, K] with unit column stride and K % 8 == 0 (K={m_dim})")
+    nblk = int(packed.shape[0])
+    if (m_dim + BLOCK_K - 1) // BLOCK_K != nblk:
+        raise ValueError(f"x has K={m_dim} but the packed weight has {nblk} K-blocks")
     kk = max(0, min(int(k), nblk))
     if idx_out is None:
         idx_out = torch.empty(max(kk, 1), dtype=torch.int32, device=dev)
@@ -89,9 +100,9 @@ def select_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
     pl = resolve_plan(bt, n_dim, nblk, kk, dev, plan)
     sel_bytes = int(lib.bsg_select_workspace_bytes(m_dim))
     gemm_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
-    ws = _workspace(f"{cache_prefix}_ws", dev, sel_bytes + gemm_bytes)
+    ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes)
     with torch.cuda.device(dev):
-        check(lib.bsg_select_gemm(x2d.data_ptr(), x2d.stride(0), bt, m_dim, int(k), entry.packed.data_ptr(), n_dim,
+        check(lib.bsg_select_gemm(x2d.data_ptr(), x2d.stride(0), bt, m_dim, int(k), packed.data_ptr(), n_dim,
                                   idx_out.data_ptr(), count_out.data_ptr(), y2d.data_ptr(), y2d.stride(0),
                                   _dtype_code(x2d), ws.data_ptr(), sel_bytes + gemm_bytes, ctypes_byref(pl),
                                   _stream_handle(dev)))

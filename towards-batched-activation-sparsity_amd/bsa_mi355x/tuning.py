@@ -29,7 +29,9 @@ from ._lib import BLOCK_K, Plan
 
 TABLE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tuned_plans.json")
 
-LLAMA2_7B_SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
+LLAMA2_7B_SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096),
+                    # q/k/v and gate/up fused along N (one GEMM per shared input and mask)
+                    "qkv_fused": (4096, 12288), "gate_up_fused": (4096, 22016)}
 
 _TABLE: Optional[List[dict]] = None
 _INDEX: Dict[Tuple[int, int], List[dict]] = {}

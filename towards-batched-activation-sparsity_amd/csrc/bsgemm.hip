@@ -128,51 +128,27 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* scratch, int* total
   return base + incl - v;
 }
 
-// Split-K hand-off primitives.  BSG_SPLITK_FENCES=1 selects full agent-scope fences
-// (L2 write-back + invalidate on every work-group); the default moves partials with
-// agent-scope relaxed atomics, which are device-coherent without touching the rest of L2.
-#ifndef BSG_SPLITK_FENCES
-#define BSG_SPLITK_FENCES 0
-#endif
+// Split-K hand-off primitives.  Partials move with agent-scope relaxed atomics, which are
+// device-coherent without touching the rest of L2 (an agent-scope fence would write back and
+// invalidate the whole L2 of the XCD on every work-group).
 
 __device__ __forceinline__ void part_store(float* p, float v) {
-#if BSG_SPLITK_FENCES
-  *p = v;
-#else
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#endif
 }
 
 // Components of one fragment lane sit 64 floats apart (see the partial layout).
 __device__ __forceinline__ f32x4 part_load(const float* q) {
   f32x4 v;
-#if BSG_SPLITK_FENCES
-  v.x = q[0];
-  v.y = q[64];
-  v.z = q[128];
-  v.w = q[192];
-#else
   v.x = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   v.y = __hip_atomic_load(q + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   v.z = __hip_atomic_load(q + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   v.w = __hip_atomic_load(q + 192, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#endif
   return v;
 }
 
 // Every store of this wave has completed (at the scope it was issued with).
 __device__ __forceinline__ void part_publish() {
-#if BSG_SPLITK_FENCES
-  __threadfence();
-#else
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt(7), lgkmcnt(15)
-#endif
-}
-
-__device__ __forceinline__ void part_acquire() {
-#if BSG_SPLITK_FENCES
-  __threadfence();
-#endif
 }
 
 __device__ __forceinline__ unsigned counter_add(uint32_t* c) {
@@ -299,7 +275,6 @@ __device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_l
   }
   __syncthreads();
   if (!*s_flag) return;
-  part_acquire();
   // Work items (fragment, split) of this wave are requested 16 at a time before any is
   // consumed (one memory round trip per 16), then summed per fragment in split order.
   const float* base = (const float*)p.part + (tile_lin * S) * FT * 256 + lane;
@@ -662,17 +637,21 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
   if (lane == 0) s_part[w] = acc;
   __syncthreads();
   if (tid == 0) {
-    p.scores[j] = s_part[0] + s_part[1] + s_part[2] + s_part[3];
-    __threadfence();
-    const unsigned prev = atomicAdd(p.cnt, 1u);
+    // Score out through an agent-scope (device-coherent) store; once it has completed, count
+    // the arrival.  The last work-group reads every score with agent-scope loads.  No L2
+    // write-back/invalidate is involved.
+    __hip_atomic_store(&p.scores[j], s_part[0] + s_part[1] + s_part[2] + s_part[3], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    const unsigned prev = __hip_atomic_fetch_add(p.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (unsigned)(p.nblk - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
 
   const int nb = p.nblk;
-  for (int i = tid; i < nb; i += 256) s_sc[i] = p.scores[i];
+  for (int i = tid; i < nb; i += 256)
+    s_sc[i] = __hip_atomic_load(&p.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const int per = (nb + 255) / 256;
   const int beg = tid * per < nb ? tid * per : nb;
@@ -699,7 +678,7 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
     if (selmask & (1ull << (jj - beg))) p.idx_out[o++] = jj;
   if (tid == 0) {
     *p.na_out = k;
-    *p.cnt = 0u;
+    __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
