@@ -53,11 +53,14 @@ enum bsg_status {
  *   cols_per_wave   : output columns per wavefront: 16, 32, 64 or 128
  *   waves_per_group : wavefronts per work-group: 1, 2, 4 or 8
  *   depth           : K-blocks whose loads each wave keeps in flight: 1, 2, 4 or 8
- *   rows_per_group  : batch rows per work-group (16, 32 or 64); bt above it adds grid rows
+ *   rows_per_group  : batch rows per work-group (16, 32 or 64; 1, 2, 4 or 8 for kind 3); bt
+ *                     above it adds grid rows
  *   kind            : 1 = the waves of a work-group split its block list (each loads its own
  *                     activation fragments); 2 = the waves split the work-group's columns and
  *                     share each block's activation tile through LDS (work-group columns =
- *                     cols_per_wave * waves_per_group)
+ *                     cols_per_wave * waves_per_group); 3 = fp32 dot products instead of MFMA
+ *                     for 1-8 rows, the work-group's activations staged in LDS once, split_k 1,
+ *                     only when named (automatic plans take kinds 1-2)
  * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
  * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
 typedef struct bsg_plan {

@@ -55,13 +55,27 @@ def test_plan_resolve_auto_fills_every_field():
     assert p.depth in (1, 2, 4, 8) and p.rows_per_group == 16 and p.kind == 1
     assert _resolve(64, 4096, 64, 31)[1].rows_per_group == 64 and _resolve(64, 4096, 64, 31)[1].kind == 2
     assert _resolve(2, 4096, 64, 0)[1].split_k == 1
+    # automatic plans use MFMA (kind 1) for small batches; kind 3 (dot products) when named,
+    # with the batch rounded up to a power of two and enough waves to stage the list
+    rc, p = _resolve(3, 4096, 64, 13)
+    assert rc == 0 and (p.kind, p.rows_per_group) == (1, 16)
+    rc, p = _resolve(3, 4096, 64, 13, plan=_lib.Plan(0, 0, 0, 0, 0, 3))
+    assert rc == 0 and (p.kind, p.rows_per_group, p.split_k, p.waves_per_group) == (3, 4, 1, 4)
+    rc, p = _resolve(2, 11008, 172, 172, plan=_lib.Plan(0, 0, 0, 0, 0, 3))
+    assert rc == 0 and (p.kind, p.rows_per_group, p.waves_per_group) == (3, 2, 4)
+    rc, p = _resolve(4, 11008, 172, 172, plan=_lib.Plan(0, 0, 0, 0, 0, 3))
+    assert rc == 0 and (p.kind, p.rows_per_group, p.waves_per_group) == (3, 4, 8)
 
 
 def test_plan_resolve_rejects():
     assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 4))[0] == _lib.BSG_ERR_UNSUPPORTED
+    # kind 3: no split-K, 1-8 rows, and its activation staging must hold the list
+    assert _resolve(4, 4096, 64, 8, plan=_lib.Plan(2, 0, 0, 0, 0, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(4, 4096, 64, 8, plan=_lib.Plan(0, 0, 0, 0, 16, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(8, 4096, 2048, 2048, plan=_lib.Plan(0, 0, 0, 0, 0, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(300, 0, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert "plan" in _lib.last_error()
 

@@ -110,7 +110,8 @@ def test_duplicate_ids_accumulate_twice(dev):
 
 
 def test_every_instantiated_tile(dev):
-    """Every compiled (rows, cols, waves, depth) kernel, split-K 1 and 3, fp16 and bf16."""
+    """Every compiled (rows, cols, waves, depth) kernel, split-K 1 and 3 (kind 3: 1 only), fp16
+    and bf16; bt=37 gives kind 3 (at most 8 rows per work-group) several row groups."""
     bt, k, n, na = 37, 4096, 1000, 29
     x, w_nk, idx = case(13, bt, k, n, na)
     ref = orc.gemm_ref64(x, w_nk, idx)
@@ -124,7 +125,7 @@ def test_every_instantiated_tile(dev):
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     packed_b = bsa.pack_weight(wb.to(dev))
     for kind, rows, cols, waves, depth in tiles:
-        for sk in (1, 3):
+        for sk in ((1,) if kind == 3 else (1, 3)):
             # explicit plan through gemm_packed, so rows_per_group is honoured even when < bt
             out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
             p = bsa.Plan(sk, cols, waves, depth, rows, kind)
@@ -134,7 +135,8 @@ def test_every_instantiated_tile(dev):
             assert_close(out.float().cpu().numpy(), ref, f"tile {kind},{rows},{cols},{waves},{depth} sk={sk}")
         # bf16 once per tile (split-K 2)
         out_b = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
-        bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b, plan=bsa.Plan(2, cols, waves, depth, rows, kind),
+        bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b,
+                        plan=bsa.Plan(1 if kind == 3 else 2, cols, waves, depth, rows, kind),
                         workspace_prefix="tiles_bf")
         torch.cuda.synchronize()
         yb = out_b.float().cpu().numpy()
@@ -142,6 +144,21 @@ def test_every_instantiated_tile(dev):
         rf = orc.rel_frobenius(yb, ref_bf)
         assert rf <= 5e-3 and np.max(np.abs(yb - ref_bf)) <= 2e-2 * np.max(np.abs(ref_bf)), \
             f"bf16 tile {kind},{rows},{cols},{waves},{depth}: rel_fro={rf:.3e}"
+
+
+@pytest.mark.parametrize("bt,rows,n_keep", [(1, 1, 34), (3, 4, 172), (4, 4, 172), (8, 8, 40)])
+def test_dot_product_kernel(dev, bt, rows, n_keep):
+    """Kind 3 (fp32 dot products, activations staged in LDS): the down shape dense at 4 rows
+    stages 88 KiB of activations (above 64 KiB of LDS)."""
+    k, n = 11008, 4096
+    x, w_nk, idx = case(31 + bt, bt, k, n, n_keep)
+    xt, it = to_dev(x, dev), to_dev(idx, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+    pl = bsa.gemm_packed(xt, packed, n, it, out, plan=bsa.Plan(0, 0, 0, 0, 0, 3), workspace_prefix="dot")
+    torch.cuda.synchronize()
+    assert (pl.kind, pl.rows_per_group) == (3, rows)
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx), f"kind 3 bt={bt} na={n_keep}")
 
 
 @pytest.mark.parametrize("split_k", [1, 2, 4, 7, 16, 29])

@@ -144,12 +144,17 @@ def nearest_density_cfg(table: Dict[float, dict], density: float) -> Tuple[float
 
 def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
     """Every instantiated tile for the batch bucket x split-K factors that leave >= 1 block per
-    list splitter."""
+    list splitter, plus the dot-product tiles (kind 3, no split-K) for batches of up to 8 rows."""
     from .runtime import kernel_tiles
 
     rb = rows_bucket(bt)
+    fma_rows = 1 << max(0, (int(bt) - 1).bit_length()) if bt <= 8 else 0
     out = []
     for kind, rows, cols, waves, depth in kernel_tiles():
+        if kind == 3:
+            if rows == fma_rows:
+                out.append(Plan(1, cols, waves, depth, rows, kind))
+            continue
         if rows != rb:
             continue
         for sk in (1, 2, 3, 4, 6, 8):

@@ -54,12 +54,18 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kOOB = (int)0x80000000u;  // buffer offset beyond any num_records we build
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 
 enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2 };
+
+// Kind 3 activation staging: 1 KiB loads per wave, and the LDS it may take.
+#define BSG_FMA_X_LOADS 16
+#define BSG_FMA_LDS_MAX (96 * 1024)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_bytes, kRsrcWord3);
@@ -89,6 +95,10 @@ struct Elem<_Float16> {
   static __device__ __forceinline__ uint16_t bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
   }
+  // a.lo*b.lo + a.hi*b.hi + c: fp16 products are exact in fp32, one fp32 rounding per add.
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  }
 };
 
 template <>
@@ -99,6 +109,9 @@ struct Elem<__bf16> {
   }
   static __device__ __forceinline__ uint16_t bits(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
   }
 };
 
@@ -562,6 +575,167 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
   if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
 }
 
+// Kind 3 ("fma", batch tiles of 1-8 rows): the contraction is too thin for MFMA, so each lane
+// multiplies the 8 consecutive channels of one weight column that its 16-byte load of the packed
+// tile holds (channels 32h + 8g .. +7 of column c, g = lane / 16, c = lane % 16) with the same
+// channels of every batch row, in fp32 with packed fp16/bf16 dot products, and the four lanes
+// of a column (g = 0..3) are summed once at the end.  The work-group's activations (its whole
+// block list, BT rows x 64 channels per block) are staged in LDS once at the start, in
+// [block][row][half h][group g] 16-byte order, so each of those reads is a broadcast; the loop
+// then streams weights only.  The waves split the work-group's block list (as kind 1) and are
+// reduced through LDS in wave order.
+template <typename T, int BT, int NSUB, int WPG, int DEPTH>
+__global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
+  constexpr int NT = 64 * WPG;
+  constexpr int XI = BSG_FMA_X_LOADS;  // staging loads per wave (host guarantees enough)
+  __shared__ int s_ids[BSG_MAX_NBLK];
+  __shared__ float s_red[WPG > 1 ? WPG - 1 : 1][NSUB * BT][16];
+  __shared__ int s_misc[WPG + 2];
+  extern __shared__ __attribute__((aligned(16))) u32x4 s_xs[];  // [na][BT][2][4]
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x;
+  const int n0 = tile * (16 * NSUB);
+  const int y0 = blockIdx.y * BT;
+
+  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  const int pbeg = (int)(((int64_t)na * w) / WPG);
+  const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
+  const int cnt = pend - pbeg;
+
+  // Stage X: 16-byte piece e = (q*BT + b)*8 + (4h + g) of the list holds x[y0+b][64 ids[q] + 32h + 8g ..];
+  // wave w loads pieces (i*WPG + w)*64 + lane, i < nxi.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const int pieces = na * BT * 8;
+  const int nxi = (pieces + NT - 1) / NT;
+  int qid[XI];  // block id of each staged piece, read as one batch
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int q = ((i * WPG + w) * 64 + lane) / (BT * 8);
+    qid[i] = s_ids[q < na ? q : 0];
+  }
+  const int blk_bytes = p.npad * 128;
+  const int wcol = lane * 16 + tile * NSUB * 2048;
+  u32x4 wv[DEPTH][NSUB][2];
+  float acc[NSUB][BT];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int b = 0; b < BT; ++b) acc[s][b] = 0.f;
+
+  auto issue = [&](u32x4 (&wd)[NSUB][2], int t) {
+    const int qq = t < cnt ? pbeg + t : 0;
+    int blk = s_ids[qq];
+    blk = __builtin_amdgcn_readfirstlane(blk);
+    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
+      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
+    }
+  };
+
+  // The first weight loads go out ahead of the staging loads: the first block needs both.
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
+  u32x4 xs[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    if (i < nxi) {
+      const int e = (i * WPG + w) * 64 + lane;
+      const int blk = e < pieces ? qid[i] : -1;
+      const int row = y0 + (e / 8) % BT;
+      const int col = blk * 64 + (e & 7) * 8;
+      const bool v = blk >= 0 && blk < p.nblk && row < p.bt && col < p.K;
+      xs[i] = ld16(xr, v ? row * (int)p.ldx * 2 + col * 2 : kOOB);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int e = (i * WPG + w) * 64 + lane;
+    if (i < nxi && e < pieces) s_xs[e] = xs[i];
+  }
+  __syncthreads();
+
+  // The X pieces of a block are read from LDS XD blocks ahead of its dot products (LDS latency
+  // off the per-block path); XD shrinks as the batch tile grows to bound the registers.
+  constexpr int XD = BT >= 8 ? 1 : (BT >= 4 ? 2 : DEPTH);
+  static_assert(DEPTH % XD == 0, "X prefetch distance");
+  const int g = lane >> 4;
+  u32x4 xv[XD][2][BT];
+  auto xread = [&](u32x4 (&xd)[2][BT], int t) {
+    // Positions past the slice carry zero weights; read a valid X piece for them.
+    const int q = pbeg + (t < cnt ? t : cnt - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < BT; ++b) xd[h][b] = s_xs[((q * BT + b) * 2 + h) * 4 + g];
+  };
+  auto compute = [&](const u32x4 (&wd)[NSUB][2], const u32x4 (&xd)[2][BT]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < BT; ++b)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+          float a = acc[s][b];
+          a = Elem<T>::dot2(wd[s][h].x, xd[h][b].x, a);
+          a = Elem<T>::dot2(wd[s][h].y, xd[h][b].y, a);
+          a = Elem<T>::dot2(wd[s][h].z, xd[h][b].z, a);
+          acc[s][b] = Elem<T>::dot2(wd[s][h].w, xd[h][b].w, a);
+        }
+  };
+
+  if (cnt > 0) {
+#pragma unroll
+    for (int k = 0; k < XD; ++k) xread(xv[k], k);
+    for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute(wv[d], xv[d % XD]);
+        xread(xv[d % XD], t0 + d + XD);
+        issue(wv[d], t0 + d + DEPTH);
+      }
+    }
+  }
+
+  // Column c of subtile s: the lanes c, c+16, c+32, c+48 hold its four channel groups.
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      float v = acc[s][b];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[s][b] = v;
+    }
+  if constexpr (WPG > 1) {
+    if (w > 0 && lane < 16) {
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+        for (int b = 0; b < BT; ++b) s_red[w - 1][s * BT + b][lane] = acc[s][b];
+    }
+    __syncthreads();
+  }
+  if (w == 0 && lane < 16) {
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      const int n = n0 + 16 * s + lane;
+#pragma unroll
+      for (int b = 0; b < BT; ++b) {
+        float v = acc[s][b];
+        for (int ww = 1; ww < WPG; ++ww) v += s_red[ww - 1][s * BT + b][lane];
+        const int row = y0 + b;
+        if (row < p.bt && n < p.N) ((uint16_t*)p.y)[(size_t)row * (size_t)p.ldy + n] = Elem<T>::bits(v);
+      }
+    }
+  }
+}
+
 // Pack W (logical [N,K], element strides sn/sk) into the tiled K-major layout.
 // One thread per 8-element (16-byte) group of the packed slab.
 __global__ __launch_bounds__(256) void bsg_pack_kernel(const uint16_t* __restrict__ w, int64_t N,
@@ -687,17 +861,19 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
 
 typedef void (*GemmFn)(GemmParams);
 
-enum { KIND_KSPLIT = 1, KIND_XLDS = 2 };
+enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3 };
 
 struct KernelEntry {
-  int kind, btt, nsub, wpg, depth;
+  int kind, rows, nsub, wpg, depth;
   GemmFn f16, bf16;
 };
 
 #define BSG_K(B, S, W, D) \
-  {KIND_KSPLIT, B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
+  {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
 #define BSG_X(B, S, W, D) \
-  {KIND_XLDS, B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, D>}
+  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, D>}
+#define BSG_F(R, S, W, D) \
+  {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D>, bsg_gemm_fma_kernel<__bf16, R, S, W, D>}
 
 // Instantiated tile set.  Kind 1 registers per lane ~ depth*(nsub+btt)*8 + btt*nsub*4;
 // kind 2 ~ depth*(nsub*8 + ceil(2*btt/wpg)*4) + btt*nsub*4.
@@ -726,14 +902,32 @@ const KernelEntry kKernels[] = {
     BSG_X(2, 1, 2, 4), BSG_X(2, 1, 4, 4), BSG_X(2, 1, 4, 8), BSG_X(2, 2, 2, 4), BSG_X(2, 2, 4, 4),
     BSG_X(4, 1, 2, 4), BSG_X(4, 1, 4, 4), BSG_X(4, 1, 4, 8), BSG_X(4, 1, 8, 4), BSG_X(4, 2, 2, 2),
     BSG_X(4, 2, 2, 4), BSG_X(4, 2, 4, 2), BSG_X(4, 2, 4, 4), BSG_X(4, 4, 2, 2), BSG_X(4, 4, 4, 2),
+    // kind 3 (fp32 dot products, 1-8 batch rows, X staged in LDS)
+    BSG_F(1, 1, 2, 4), BSG_F(1, 1, 4, 4), BSG_F(1, 1, 4, 8), BSG_F(1, 1, 8, 4), BSG_F(1, 2, 4, 4),
+    BSG_F(2, 1, 2, 4), BSG_F(2, 1, 4, 4), BSG_F(2, 1, 4, 8), BSG_F(2, 1, 8, 4), BSG_F(2, 2, 4, 4),
+    BSG_F(4, 1, 2, 4), BSG_F(4, 1, 4, 4), BSG_F(4, 1, 4, 8), BSG_F(4, 1, 8, 4), BSG_F(4, 2, 4, 4),
+    BSG_F(8, 1, 2, 4), BSG_F(8, 1, 4, 4), BSG_F(8, 1, 4, 8), BSG_F(8, 1, 8, 4), BSG_F(8, 2, 4, 4),
 };
 #undef BSG_K
 #undef BSG_X
+#undef BSG_F
 
-const KernelEntry* find_kernel(int kind, int btt, int nsub, int wpg, int depth) {
+const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
   for (const KernelEntry& e : kKernels)
-    if (e.kind == kind && e.btt == btt && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
+    if (e.kind == kind && e.rows == rows && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
   return nullptr;
+}
+
+// Kind 3 stages the work-group's whole list of activation blocks in LDS with at most
+// BSG_FMA_X_LOADS 1 KiB loads per wave: na * rows pieces of 128 B.
+bool fma_fits(int64_t na, int rows, int wpg) {
+  return na * rows <= (int64_t)BSG_FMA_X_LOADS * 8 * wpg && na * rows * 128 <= BSG_FMA_LDS_MAX;
+}
+
+int pow2_ceil(int64_t v) {
+  int r = 1;
+  while (r < v) r <<= 1;
+  return r;
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -745,17 +939,44 @@ int64_t group_cols(const bsg_plan* pl) {
   return (int64_t)pl->cols_per_wave * (pl->kind == KIND_XLDS ? pl->waves_per_group : 1);
 }
 
+int resolve_fma(int64_t bt, int32_t na, bsg_plan* pl) {
+  if (pl->rows_per_group != 1 && pl->rows_per_group != 2 && pl->rows_per_group != 4 && pl->rows_per_group != 8)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind 3 rows_per_group=%d (1, 2, 4 or 8)", pl->rows_per_group);
+  if (pl->split_k == 0) pl->split_k = 1;
+  if (pl->split_k != 1) return fail(BSG_ERR_UNSUPPORTED, "plan: kind 3 needs split_k=1 (got %d)", pl->split_k);
+  if (pl->cols_per_wave == 0) pl->cols_per_wave = 16;
+  if (pl->depth == 0) pl->depth = 4;
+  if (pl->waves_per_group == 0) {
+    pl->waves_per_group = 4;
+    while (pl->waves_per_group < 8 && !fma_fits(na, pl->rows_per_group, pl->waves_per_group))
+      pl->waves_per_group *= 2;
+  }
+  if (!fma_fits(na, pl->rows_per_group, pl->waves_per_group))
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind 3 stages %d blocks x %d rows, more than %d waves can (use kind 1)",
+                na, pl->rows_per_group, pl->waves_per_group);
+  if (!find_kernel(KIND_FMA, pl->rows_per_group, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
+    return fail(BSG_ERR_UNSUPPORTED, "plan: no kind 3 kernel for rows_per_group=%d cols_per_wave=%d "
+                "waves_per_group=%d depth=%d", pl->rows_per_group, pl->cols_per_wave, pl->waves_per_group,
+                pl->depth);
+  return BSG_OK;
+}
+
 int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_plan* pl) {
   if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
     return fail(BSG_ERR_ARG, "plan: bt=%lld N=%lld nblk=%d na=%d cu=%d", (long long)bt, (long long)N,
                 nblk, na, cu);
+  if (pl->kind < 0 || pl->kind > KIND_FMA)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X tile in LDS, "
+                "3 = fp32 dot products for 1-8 rows)", pl->kind);
+  // The dot-product kernel (kind 3) runs when a plan names it; automatic plans use the MFMA
+  // kinds, which measure faster at every batch size on gfx950.
+  if (pl->rows_per_group == 0 && pl->kind == KIND_FMA) pl->rows_per_group = bt <= 8 ? pow2_ceil(bt) : 8;
   if (pl->rows_per_group == 0) pl->rows_per_group = bt <= 16 ? 16 : (bt <= 32 ? 32 : 64);
   const int rpg = pl->rows_per_group;
+  if (pl->kind == 0) pl->kind = rpg <= 8 ? KIND_FMA : (rpg == 16 ? KIND_KSPLIT : KIND_XLDS);
+  if (pl->kind == KIND_FMA) return resolve_fma(bt, na, pl);
   if (rpg != 16 && rpg != 32 && rpg != 64)
-    return fail(BSG_ERR_UNSUPPORTED, "plan: rows_per_group=%d (16, 32 or 64)", rpg);
-  if (pl->kind == 0) pl->kind = rpg == 16 ? KIND_KSPLIT : KIND_XLDS;
-  if (pl->kind != KIND_KSPLIT && pl->kind != KIND_XLDS)
-    return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X in LDS)", pl->kind);
+    return fail(BSG_ERR_UNSUPPORTED, "plan: rows_per_group=%d (16, 32 or 64 for kinds 1-2)", rpg);
   const int auto_fields = (pl->cols_per_wave == 0 ? 1 : 0) | (pl->waves_per_group == 0 ? 2 : 0) |
                           (pl->depth == 0 ? 4 : 0);
   if (pl->kind == KIND_KSPLIT) {
@@ -771,14 +992,14 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
       !pow2_in(pl->depth, 1, 8))
     return fail(BSG_ERR_UNSUPPORTED, "plan: cols_per_wave=%d waves_per_group=%d depth=%d",
                 pl->cols_per_wave, pl->waves_per_group, pl->depth);
-  if (!find_kernel(pl->kind, rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth) &&
+  if (!find_kernel(pl->kind, rpg, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth) &&
       auto_fields) {
     // An automatic field led to a tile that is not compiled: take the instantiated kernel
     // that keeps every explicit field and is closest in the automatic ones.
     const KernelEntry* best = nullptr;
     int best_d = 1 << 30;
     for (const KernelEntry& e : kKernels) {
-      if (e.kind != pl->kind || e.btt != rpg / 16) continue;
+      if (e.kind != pl->kind || e.rows != rpg) continue;
       if (!(auto_fields & 1) && e.nsub * 16 != pl->cols_per_wave) continue;
       if (!(auto_fields & 2) && e.wpg != pl->waves_per_group) continue;
       if (!(auto_fields & 4) && e.depth != pl->depth) continue;
@@ -795,7 +1016,7 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
       pl->depth = best->depth;
     }
   }
-  if (!find_kernel(pl->kind, rpg / 16, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
+  if (!find_kernel(pl->kind, rpg, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
     return fail(BSG_ERR_UNSUPPORTED,
                 "plan: no kernel instantiated for kind=%d rows_per_group=%d cols_per_wave=%d "
                 "waves_per_group=%d depth=%d",
@@ -892,7 +1113,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
     return fail(BSG_ERR_WORKSPACE, "workspace %lld bytes < %lld needed (split_k=%d)", (long long)ws_bytes,
                 (long long)need, pl.split_k);
   const KernelEntry* ke =
-      find_kernel(pl.kind, pl.rows_per_group / 16, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
+      find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
   const int64_t npad = cdiv(N, 16) * 16;
   const int64_t n_tiles = cdiv(npad, group_cols(&pl));
   const int64_t ygroups = cdiv(bt, pl.rows_per_group);
@@ -927,7 +1148,10 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
   GemmFn fn = dtype == BSG_F16 ? ke->f16 : ke->bf16;
-  hipLaunchKernelGGL(fn, grid, block, 0, (hipStream_t)stream, p);
+  // Kind 3: LDS for the staged activations of the whole list (na is the list capacity; a
+  // device-side count or a bitmap only shortens it).
+  const size_t dyn_lds = pl.kind == KIND_FMA ? (size_t)na * (size_t)pl.rows_per_group * 128 : 0;
+  hipLaunchKernelGGL(fn, grid, block, dyn_lds, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bsg_gemm launch");
   return BSG_OK;
