@@ -150,6 +150,33 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
                        int32_t* idx_out, int32_t* na_out, int dtype,
                        void* ws, int64_t ws_bytes, void* stream);
 
+/* Selector with the reference's own scoring rules (scripts/bench_roundrobin_e2e_decode.py,
+ * RRD:90-176), computed in fp64.  Scored blocks are floor(K/64), as there.
+ *   score         : BSG_SCORE_L2_MEAN  mean over rows of the block's L2 norm   (RRD:100)
+ *                   BSG_SCORE_ENERGY   mean over rows of sum x^2 [* channel_scale]  (RRD:103-105)
+ *                   BSG_SCORE_L1       the exact L1 rule of bsg_select_topk_l1 (no other option)
+ *   block_prior   : score *= max(prior + prior_eps, 1e-6)^prior_alpha            (RRD:106-112)
+ *   energy_keep   : > 0 keeps more than k blocks, up to the first rank whose cumulative
+ *                   energy (unscaled, in score order) reaches energy_keep of the total; idx_out
+ *                   then needs room for floor(K/64) entries                     (RRD:155-176)
+ *   ratio_out     : kept energy fraction (float, device), as RRD:141 / RRD:176 return it
+ * Ranking is (score desc, block id asc); idx_out holds the kept ids ascending and *na_out
+ * their count, both on the device.  Workspace as bsg_select_topk_l1.  Replaces
+ * _select_active_blocks (RRD:90-113), _topk_energy_ratio (RRD:116-141) and
+ * _energy_expanded_active_blocks (RRD:144-176). */
+enum bsg_score { BSG_SCORE_L1 = 0, BSG_SCORE_L2_MEAN = 1, BSG_SCORE_ENERGY = 2 };
+typedef struct bsg_select_opts {
+  int32_t score;
+  float energy_keep;
+  const float* block_prior;
+  float prior_alpha;
+  float prior_eps;
+  const float* channel_scale;
+  float* ratio_out;
+} bsg_select_opts;
+int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
+                    int32_t* idx_out, int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream);
+
 /* Selector followed by the GEMM on its device-side list, both on `stream`.
  * ws is split: the first bsg_select_workspace_bytes(K) bytes for the selector, the rest
  * (bsg_gemm_workspace_bytes) for the GEMM.  Replaces the select -> bitmap -> GEMM sequence

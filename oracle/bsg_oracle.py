@@ -166,6 +166,83 @@ def select_l2_mean_ref(x: np.ndarray, density: float) -> np.ndarray:
     return np.sort(np.asarray(order[:nk], dtype=np.int32))
 
 
+def block_stats64(x: np.ndarray, scale=None):
+    """Per whole block j < floor(K/64) (RRD:97-99), in float64: the batch mean of the per-row
+    L2 norm (RRD:100), of the energy sum x^2 (RRD:131, 156), and of the channel-scaled energy
+    sum x^2 * scale_c (RRD:103-105)."""
+    bt, kdim = x.shape
+    nb = kdim // BLOCK_K
+    xb = np.asarray(x, dtype=np.float64)[:, : nb * BLOCK_K].reshape(bt, nb, BLOCK_K)
+    sq = xb * xb
+    l2 = np.sqrt(sq.sum(axis=2)).mean(axis=0)
+    energy = sq.sum(axis=2).mean(axis=0)
+    if scale is None:
+        return l2, energy, energy
+    sc = np.asarray(scale, dtype=np.float64)[: nb * BLOCK_K].reshape(1, nb, BLOCK_K)
+    return l2, energy, (sq * sc).sum(axis=2).mean(axis=0)
+
+
+def select_scored_ref(x: np.ndarray, k: int, score: str = "l2_mean", prior=None, alpha: float = 1.0,
+                      eps: float = 0.1, scale=None, energy_keep: float = 0.0):
+    """The reference's scoring rules (RRD:90-176) in float64, ranking by (score desc, id asc):
+      score  = l2 (RRD:100) or energy [* scale] (RRD:103-105, 131), times
+               max(prior + eps, 1e-6)^alpha when a prior is given (RRD:106-112);
+      keep   = min(k, nblk), grown while energy_keep > 0 and the top-keep energy share is below
+               it, to searchsorted(cum, energy_keep * total) + 1 clamped to [k, nblk] (RRD:165-176);
+      ratio  = cumulative energy at keep / max(total, 1e-12) (RRD:141, 176).
+    Returns (ids ascending int32, keep, ratio)."""
+    l2, energy, es = block_stats64(x, scale)
+    nb = len(energy)
+    sc = (l2 if score == "l2_mean" else es).copy()
+    if prior is not None:
+        pr = np.asarray(prior, dtype=np.float64)[:nb] + float(eps)
+        sc = sc * np.maximum(pr, 1e-6) ** float(alpha)
+    order = sorted(range(nb), key=lambda j: (-float(sc[j]), j))
+    k0 = max(0, min(int(k), nb))
+    cum = np.cumsum(energy[order])
+    total = max(float(energy.sum()), 1e-12)
+    keep = k0
+    if energy_keep > 0 and k0 > 0 and cum[k0 - 1] / total < energy_keep:
+        first = int(np.searchsorted(cum, energy_keep * total, side="left"))
+        keep = max(k0, min(nb, first + 1))
+    ratio = float(cum[keep - 1] / total) if keep > 0 else 0.0
+    return np.sort(np.asarray(order[:keep], dtype=np.int32)), keep, ratio
+
+
+def select_scored_torch32(x, k: int, score: str = "l2_mean", prior=None, alpha: float = 1.0, eps: float = 0.1,
+                          scale=None, energy_keep: float = 0.0):
+    """The same rules written the way the reference evaluates them: torch CPU float32,
+    torch.topk / argsort / cumsum / searchsorted (RRD:97-113, 127-141, 151-176).  Pins
+    select_scored_ref on inputs without near-ties (torch's tie order is unspecified)."""
+    import torch
+
+    x3 = torch.as_tensor(np.asarray(x)).reshape(x.shape[0], 1, x.shape[-1])
+    total_k = x3.shape[-1] // BLOCK_K
+    xb = x3[..., : total_k * BLOCK_K].float().reshape(-1, total_k, BLOCK_K)
+    energy = xb.pow(2).sum(dim=2).mean(dim=0)
+    if score == "l2_mean":
+        sc = xb.norm(dim=2).mean(dim=0)
+    elif scale is None:
+        sc = energy
+    else:
+        sc = (xb.pow(2) * torch.as_tensor(np.asarray(scale, dtype=np.float32))[: total_k * BLOCK_K]
+              .reshape(1, total_k, BLOCK_K)).sum(dim=2).mean(dim=0)
+    if prior is not None:
+        sc = sc * torch.clamp(torch.as_tensor(np.asarray(prior, dtype=np.float32)) + float(eps), min=1e-6).pow(
+            float(alpha))
+    k0 = max(0, min(int(k), total_k))
+    order = torch.argsort(sc, descending=True)
+    cum = torch.cumsum(energy[order], dim=0)
+    total = max(float(energy.sum().item()), 1e-12)
+    keep = k0
+    if energy_keep > 0 and k0 > 0 and float(cum[k0 - 1].item() / total) < float(energy_keep):
+        first = int(torch.searchsorted(cum, torch.tensor(float(energy_keep) * total)).item())
+        keep = max(k0, min(total_k, first + 1))
+    ids = torch.topk(sc, k=keep).indices.sort()[0].to(torch.int32).numpy()
+    ratio = float(cum[keep - 1].item() / total) if keep > 0 else 0.0
+    return ids, keep, ratio
+
+
 def n_keep(density: float, total_k: int) -> int:
     """max(1, min(total_k, round(density * total_k))) (RRD:102, Python's round)."""
     return max(1, min(int(total_k), int(round(float(density) * int(total_k)))))

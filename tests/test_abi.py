@@ -90,7 +90,7 @@ def test_workspace_bytes():
     p = _lib.Plan(2, 16, 4, 4, 64, 2)  # kind 2: a work-group covers 16 * 4 columns
     tiles = 4096 // 64
     assert lib.bsg_gemm_workspace_bytes(64, 4096, ctypes.byref(p)) == 256 + tiles * 2 * (4 * 4) * 64 * 16
-    assert lib.bsg_select_workspace_bytes(4096) == 768
+    assert lib.bsg_select_workspace_bytes(4096) == 1280  # 256 + 64 blocks x (score, energy)
     assert lib.bsg_select_workspace_bytes(0) == -1
 
 
@@ -164,3 +164,26 @@ def test_make_plan_maps_reference_tiles():
     assert p.as_tuple() == (4, 64, 2, 4, 64, 0)   # BLOCK_B raised to cover the batch; stages -> depth 4
     assert bsa.make_plan().as_tuple() == (0, 0, 0, 0, 0, 0)
     assert bsa.n_keep_for_density(0.48, 64) == 31
+
+
+def test_select_topk_rejects_bad_options():
+    """Argument checks of bsg_select_topk run on the host (no device pointer is touched)."""
+    lib = bsa.load()
+    fake = 1 << 20  # never dereferenced: every case below fails its host checks first
+
+    def call(opts, k=4, kdim=4096):
+        rc = lib.bsg_select_topk(fake, kdim, 2, kdim, k, ctypes.byref(opts), fake, fake, 0, fake, 1 << 20, None)
+        return rc, _lib.last_error()
+
+    rc, msg = call(_lib.SelectOpts(7, 0.0, None, 1.0, 0.1, None, None))
+    assert rc == _lib.BSG_ERR_UNSUPPORTED and "score" in msg
+    rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_L1, 0.5, None, 1.0, 0.1, None, None))
+    assert rc == _lib.BSG_ERR_UNSUPPORTED
+    rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_ENERGY, 1.5, None, 1.0, 0.1, None, None))
+    assert rc == _lib.BSG_ERR_ARG and "energy_keep" in msg
+    rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_L2_MEAN, 0.0, None, 1.0, 0.1, fake, None))
+    assert rc == _lib.BSG_ERR_ARG and "channel_scale" in msg
+    rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_L2_MEAN, 0.0, None, 1.0, 0.1, None, None), kdim=32)
+    assert rc == _lib.BSG_ERR_ARG
+    rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_L2_MEAN, 0.0, None, 1.0, 0.1, None, None), k=-1)
+    assert rc == _lib.BSG_ERR_ARG

@@ -81,3 +81,89 @@ def test_select_density_wrapper(dev):
     torch.cuda.synchronize()
     assert got.dtype == torch.int32 and got.numel() == orc.n_keep(0.48, 64) == 31
     assert np.array_equal(got.cpu().numpy(), orc.select_topk_l1(x, 31))
+
+
+# ---------------------------------------------------------------------------------------
+# Reference scoring rules (L2 mean, energy, prior, channel scale, energy budget), fp64 scores:
+# the kept set and count must equal the float64 oracle's; the kept-energy ratio within 1e-6.
+
+
+def _scored(dev, x, k, dtype=torch.float16, **kw):
+    kw = {n: (to_dev(np.asarray(v, np.float32), dev, torch.float32) if isinstance(v, np.ndarray) else v)
+          for n, v in kw.items()}
+    xt = torch.from_numpy(np.asarray(x, np.float32)).to(dtype).to(dev)
+    ratio = torch.empty(1, dtype=torch.float32, device=dev)
+    idx, cnt, _ = bsa.select_topk(xt, k, ratio_out=ratio, **kw)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    return idx[:c].cpu().numpy(), c, float(ratio.item())
+
+
+@pytest.mark.parametrize("score,prior,scale,keep", [("l2_mean", False, False, 0.0), ("energy", False, False, 0.0),
+                                                    ("energy", False, True, 0.0), ("l2_mean", True, False, 0.0),
+                                                    ("energy", True, False, 0.9), ("l2_mean", False, False, 0.75)])
+@pytest.mark.parametrize("bt,kdim,k", [(1, 4096, 13), (16, 4096, 23), (64, 4096, 31), (64, 11008, 83),
+                                       (5, 1000, 4), (33, 2048, 1)])
+def test_scored_selector_matches_oracle(dev, score, prior, scale, keep, bt, kdim, k):
+    rng = np.random.default_rng(bt * 13 + k)
+    x = rng.laplace(0, 0.05, size=(bt, kdim)).astype(np.float16)
+    nb = kdim // 64
+    kw = dict(score=score, energy_keep=keep)
+    if prior:
+        kw.update(block_prior=rng.uniform(0, 1, size=nb).astype(np.float32), prior_alpha=0.7, prior_eps=0.1)
+    if scale:
+        kw["channel_scale"] = rng.uniform(0.5, 2, size=kdim).astype(np.float32)
+    got, cnt, ratio = _scored(dev, x, k, **kw)
+    want, wkeep, wratio = orc.select_scored_ref(x, k, score, prior=kw.get("block_prior"), alpha=0.7, eps=0.1,
+                                                scale=kw.get("channel_scale"), energy_keep=keep)
+    assert cnt == wkeep and np.array_equal(got, want), (cnt, wkeep)
+    assert abs(ratio - wratio) <= 1e-6 * max(wratio, 1e-12) + 1e-7
+
+
+def test_scored_selector_bf16_and_closed_form_budget(dev):
+    x = np.zeros((3, 5 * 64), dtype=np.float32)
+    for j, m in enumerate((32, 16, 8, 4, 4)):
+        x[:, 64 * j:64 * j + m] = 1.0
+    for dt in (torch.float16, torch.bfloat16):
+        got, cnt, ratio = _scored(dev, x, 1, dtype=dt, score="energy", energy_keep=0.8)
+        assert cnt == 3 and np.array_equal(got, [0, 1, 2]) and ratio == 56 / 64
+    rng = np.random.default_rng(9)
+    xb = rng.normal(0, 1, size=(16, 4096)).astype(np.float32)
+    xb16 = torch.from_numpy(xb).to(torch.bfloat16).float().numpy()  # the values the kernel sees
+    got, cnt, _ = _scored(dev, xb, 20, dtype=torch.bfloat16, score="l2_mean")
+    want, _, _ = orc.select_scored_ref(xb16, 20, "l2_mean")
+    assert np.array_equal(got, want)
+
+
+def test_reference_selector_drop_ins(dev):
+    """_select_active_blocks / _topk_energy_ratio / _energy_expanded_active_blocks keep the
+    reference's signatures (RRD:90-176) and agree with the oracle."""
+    rng = np.random.default_rng(11)
+    x = rng.laplace(0, 0.05, size=(16, 11008)).astype(np.float16)
+    x3 = to_dev(x, dev).view(16, 1, 11008)
+    idx = bsa._select_active_blocks(x3, 0.36, 64)
+    want, _, _ = orc.select_scored_ref(x, orc.n_keep(0.36, 172), "l2_mean")
+    assert np.array_equal(idx.cpu().numpy(), want)
+    r = bsa._topk_energy_ratio(x3, 0.36, 64)
+    _, _, wr = orc.select_scored_ref(x, orc.n_keep(0.36, 172), "energy")
+    assert abs(r - wr) < 1e-6
+    active, ratio, dens = bsa._energy_expanded_active_blocks(x3, 0.2, 64, 0.5)
+    want, keep, wr = orc.select_scored_ref(x, orc.n_keep(0.2, 172), "energy", energy_keep=0.5)
+    assert np.array_equal(active.cpu().numpy(), want) and abs(ratio - wr) < 1e-6 and dens == keep / 172
+    assert bsa._energy_expanded_active_blocks(x3, 1.0, 64, 0.5) == (None, 1.0, 1.0)
+
+
+def test_budget_selection_feeds_gemm_by_device_count(dev):
+    """The budget selector's device-side count drives the GEMM without a host round trip."""
+    bt, k, n = 16, 4096, 1024
+    x, w_nk, _ = case(41, bt, k, n, 1)
+    xt = to_dev(x, dev)
+    idx, cnt, _ = bsa.select_topk(xt, 8, score="energy", energy_keep=0.6)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    out = torch.empty(bt, n, dtype=torch.float16, device=dev)
+    bsa.gemm_packed(xt, packed, n, idx, out, num_active=idx.numel(), num_active_dev=cnt)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    want, keep, _ = orc.select_scored_ref(x, 8, "energy", energy_keep=0.6)
+    assert c == keep and np.array_equal(idx[:c].cpu().numpy(), want)
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, want), "budget selection -> GEMM")

@@ -173,3 +173,50 @@ def test_make_inputs_seeded():
     for u, v in zip(a, b):
         assert np.array_equal(u, v)
     assert a[1].shape == (128, 32) and a[0].dtype == np.float16 and a[2].dtype == np.int32
+
+
+@pytest.mark.parametrize("score,use_prior,use_scale", [("l2_mean", False, False), ("energy", False, False),
+                                                       ("energy", False, True), ("l2_mean", True, False),
+                                                       ("energy", True, True)])
+@pytest.mark.parametrize("bt,kdim,k", [(1, 1024, 3), (4, 4096, 13), (16, 4096, 23), (64, 11008, 83), (7, 1000, 5)])
+def test_scored_selector_matches_reference_formula(score, use_prior, use_scale, bt, kdim, k):
+    """float64 restatement == the reference formula in torch float32 (topk / argsort) on inputs
+    without near-ties; the partial block of K=1000 is never scored (floor(K/64) blocks)."""
+    rng = np.random.default_rng(bt * 31 + k)
+    x = rng.laplace(0, 0.05, size=(bt, kdim)).astype(np.float16)
+    nb = kdim // 64
+    prior = rng.uniform(0, 1, size=nb).astype(np.float32) if use_prior else None
+    scale = rng.uniform(0.5, 2, size=kdim).astype(np.float32) if use_scale else None
+    ids, keep, ratio = orc.select_scored_ref(x, k, score, prior=prior, alpha=0.7, eps=0.1, scale=scale)
+    ids32, keep32, ratio32 = orc.select_scored_torch32(x, k, score, prior=prior, alpha=0.7, eps=0.1, scale=scale)
+    assert keep == keep32 == min(k, nb) and np.array_equal(ids, ids32)
+    assert abs(ratio - ratio32) <= 1e-5 * max(ratio, 1e-12)
+    assert ids.max() < nb
+
+
+def test_energy_budget_closed_form():
+    """Block energies 32,16,8,4,4 per row (that many entries equal to 1, exact); k=1 keeps
+    32/64 = 0.5 < 0.8, the cumulative energies 32,48,56,60,64 first reach 0.8*64 = 51.2 at
+    rank 2, so blocks {0,1,2} stay, ratio 56/64."""
+    x = np.zeros((3, 5 * 64), dtype=np.float16)
+    for j, m in enumerate((32, 16, 8, 4, 4)):
+        x[:, 64 * j:64 * j + m] = 1.0
+    ids, keep, ratio = orc.select_scored_ref(x, 1, "energy", energy_keep=0.8)
+    assert keep == 3 and np.array_equal(ids, [0, 1, 2]) and ratio == 56 / 64
+    ids, keep, ratio = orc.select_scored_ref(x, 1, "energy", energy_keep=0.5)  # already met at k
+    assert keep == 1 and np.array_equal(ids, [0]) and ratio == 0.5
+    ids, keep, _ = orc.select_scored_ref(x, 2, "energy", energy_keep=1.0)  # everything
+    assert keep == 5
+    ids32, keep32, _ = orc.select_scored_torch32(x, 1, "energy", energy_keep=0.8)
+    assert keep32 == 3 and np.array_equal(ids32, [0, 1, 2])
+
+
+def test_scored_selector_ties_and_prior():
+    """Equal scores go to the lower id; a prior reorders blocks by score * (prior + eps)^alpha."""
+    x = np.ones((2, 4 * 64), dtype=np.float16)
+    ids, _, _ = orc.select_scored_ref(x, 2, "l2_mean")
+    assert np.array_equal(ids, [0, 1])
+    ids, _, _ = orc.select_scored_ref(x, 2, "l2_mean", prior=np.array([0, 0, 1, 2], np.float32), alpha=1.0, eps=0.1)
+    assert np.array_equal(ids, [2, 3])
+    ids, _, _ = orc.select_scored_ref(x, 1, "energy", prior=np.array([-5, 0, 0, 0], np.float32), alpha=2.0, eps=0.1)
+    assert np.array_equal(ids, [1])  # prior clamped to 1e-6 for block 0; ties among 1..3 -> 1

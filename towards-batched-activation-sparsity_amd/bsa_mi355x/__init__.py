@@ -17,7 +17,8 @@ from .runtime import (INDEX_BLOCK_META_SIZE, TileConfig, _build_active_k_bitmap,
                       prepacked_block_sparse_gemm_batched_kernel,
                       prepacked_block_sparse_gemm_bitmap_preload_batched_kernel, release_prepacked_weights,
                       resolve_plan)
-from .select import _select_active_blocks_l1, select_sparse_gemm, select_topk_l1
+from .select import (_energy_expanded_active_blocks, _select_active_blocks, _select_active_blocks_l1,
+                     _topk_energy_ratio, select_sparse_gemm, select_topk, select_topk_l1)
 
 __all__ = [
     "BLOCK_K", "MAX_NBLK", "INDEX_BLOCK_META_SIZE", "Plan", "TileConfig", "load",
@@ -30,5 +31,6 @@ __all__ = [
     "prepacked_block_sparse_gemm_batched_kernel", "prepacked_block_sparse_gemm_bitmap_preload_batched_kernel",
     "dense_gemm", "gemm_packed", "pack_weight", "make_plan", "resolve_plan", "kernel_tiles",
     "release_prepacked_weights", "n_keep_for_density", "active_bytes", "nblk_of",
-    "select_topk_l1", "select_sparse_gemm", "_select_active_blocks_l1",
+    "select_topk_l1", "select_topk", "select_sparse_gemm", "_select_active_blocks_l1", "_select_active_blocks",
+    "_topk_energy_ratio", "_energy_expanded_active_blocks",
 ]

@@ -68,6 +68,23 @@ class Plan(ctypes.Structure):
                 % self.as_tuple())
 
 
+BSG_SCORE_L1, BSG_SCORE_L2_MEAN, BSG_SCORE_ENERGY = 0, 1, 2
+
+
+class SelectOpts(ctypes.Structure):
+    """Mirror of `bsg_select_opts` (pointers are device addresses or None)."""
+
+    _fields_ = [
+        ("score", ctypes.c_int32),
+        ("energy_keep", ctypes.c_float),
+        ("block_prior", ctypes.c_void_p),
+        ("prior_alpha", ctypes.c_float),
+        ("prior_eps", ctypes.c_float),
+        ("channel_scale", ctypes.c_void_p),
+        ("ratio_out", ctypes.c_void_p),
+    ]
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -88,6 +105,8 @@ SIGNATURES = {
     "bsg_gemm_dense": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_select_workspace_bytes": (_i64, [_i64]),
     "bsg_select_topk_l1": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _int, _vp, _i64, _vp]),
+    "bsg_select_topk": (_int, [_vp, _i64, _i64, _i64, _i32, ctypes.POINTER(SelectOpts), _vp, _vp, _int, _vp,
+                               _i64, _vp]),
     "bsg_select_gemm": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _i64,
                                _pplan, _vp]),
 }

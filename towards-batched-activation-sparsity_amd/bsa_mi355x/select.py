@@ -65,6 +65,120 @@ def _select_active_blocks_l1(x3: torch.Tensor, density: float, block_k: int = BL
     return idx
 
 
+_SCORES = {"l1": _lib.BSG_SCORE_L1, "l2_mean": _lib.BSG_SCORE_L2_MEAN, "energy": _lib.BSG_SCORE_ENERGY}
+
+
+def _dev_f32(t: Optional[torch.Tensor], dev: torch.device, n: int, what: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    t = t.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if t.numel() < n:
+        raise ValueError(f"{what} has {t.numel()} entries, needs {n}")
+    return t
+
+
+def select_topk(x: torch.Tensor, k: int, score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
+                prior_alpha: float = 1.0, prior_eps: float = 0.1, channel_scale: Optional[torch.Tensor] = None,
+                energy_keep: float = 0.0, idx_out: Optional[torch.Tensor] = None,
+                count_out: Optional[torch.Tensor] = None, ratio_out: Optional[torch.Tensor] = None,
+                workspace_prefix: str = "select") -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Device selector with the reference's scoring rules (RRD:90-176), fp64 scores, ranking by
+    (score desc, block id asc).  x is [..., K] fp16/bf16; blocks are floor(K/64).
+
+    score "l2_mean" | "energy" | "l1"; block_prior multiplies the score by
+    max(prior + eps, 1e-6)^alpha; channel_scale ([K]) weights the energy score; energy_keep > 0
+    keeps the first ranks whose cumulative energy reaches that fraction (at least k).
+    Returns (idx int32 ascending, padded to the capacity; count int32 [1]; ratio float32 [1] or
+    None), all on the device: idx[:count] is the selection."""
+    lib = load()
+    dev = _require_cuda(x)
+    x2d = _x2d(x)
+    bt, kd = x2d.shape
+    nb = kd // BLOCK_K
+    if nb < 1:
+        raise ValueError(f"K={kd} has no whole 64-channel block")
+    if score not in _SCORES:
+        raise ValueError(f"score must be one of {sorted(_SCORES)}")
+    cap = nb if energy_keep > 0 else max(0, min(int(k), nb))
+    if score == "l1":
+        cap = max(0, min(int(k), (kd + BLOCK_K - 1) // BLOCK_K))
+    if idx_out is None:
+        idx_out = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    if count_out is None:
+        count_out = torch.empty(1, dtype=torch.int32, device=dev)
+    want_ratio = ratio_out is not None or (score != "l1" and energy_keep > 0)
+    if want_ratio and ratio_out is None:
+        ratio_out = torch.empty(1, dtype=torch.float32, device=dev)
+    prior = _dev_f32(block_prior, dev, nb, "block_prior")
+    scale = _dev_f32(channel_scale, dev, kd, "channel_scale")
+    opts = _lib.SelectOpts(_SCORES[score], float(energy_keep), prior.data_ptr() if prior is not None else None,
+                           float(prior_alpha), float(prior_eps), scale.data_ptr() if scale is not None else None,
+                           ratio_out.data_ptr() if want_ratio else None)
+    ws_bytes = int(lib.bsg_select_workspace_bytes(kd))
+    ws = _workspace(workspace_prefix, dev, ws_bytes)
+    with torch.cuda.device(dev):
+        check(lib.bsg_select_topk(x2d.data_ptr(), x2d.stride(0), bt, kd, int(k), ctypes_byref(opts),
+                                  idx_out.data_ptr(), count_out.data_ptr(), _dtype_code(x2d), ws.data_ptr(), ws_bytes,
+                                  _stream_handle(dev)))
+    return idx_out, count_out, (ratio_out if want_ratio else None)
+
+
+def _select_active_blocks(x3: torch.Tensor, density: float, block_k: int = BLOCK_K,
+                          block_prior: Optional[torch.Tensor] = None, prior_alpha: float = 1.0, prior_eps: float = 0.1,
+                          block_score_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Drop-in for `_select_active_blocks` (scripts/bench_roundrobin_e2e_decode.py:90-113): the
+    reference's score (mean L2 norm, or the channel-scaled energy when block_score_scale is
+    given; optional prior), n_keep = max(1, min(nblk, round(density * nblk))), ascending int32
+    ids on the device, one kernel launch."""
+    if int(block_k) != BLOCK_K:
+        raise ValueError(f"block_k must be {BLOCK_K}")
+    nb = x3.shape[-1] // BLOCK_K
+    nk = n_keep_for_density(density, nb)
+    idx, _, _ = select_topk(x3, nk, score="energy" if block_score_scale is not None else "l2_mean",
+                            block_prior=block_prior, prior_alpha=prior_alpha, prior_eps=prior_eps,
+                            channel_scale=block_score_scale, workspace_prefix="select_ref")
+    return idx[:nk]
+
+
+def _topk_energy_ratio(x: torch.Tensor, density: float, block_k: int = BLOCK_K,
+                       block_prior: Optional[torch.Tensor] = None, prior_alpha: float = 1.0,
+                       prior_eps: float = 0.1) -> float:
+    """Drop-in for `_topk_energy_ratio` (RRD:116-141): the fraction of the batch-mean block
+    energy kept by the top-n_keep blocks (energy score, optional prior).  Synchronises to
+    return a float, as the reference does."""
+    x3 = x.reshape(x.shape[0], 1, x.shape[-1]) if x.dim() == 2 else x
+    if x3.shape[1] != 1 or density >= 1.0:
+        return 1.0
+    if int(block_k) != BLOCK_K:
+        raise ValueError(f"block_k must be {BLOCK_K}")
+    nb = x3.shape[-1] // BLOCK_K
+    nk = n_keep_for_density(density, nb)
+    ratio = torch.empty(1, dtype=torch.float32, device=x3.device)
+    select_topk(x3, nk, score="energy", block_prior=block_prior, prior_alpha=prior_alpha, prior_eps=prior_eps,
+                ratio_out=ratio, workspace_prefix="select_ref")
+    return float(ratio.item())
+
+
+def _energy_expanded_active_blocks(x: torch.Tensor, density: float, block_k: int, energy_keep: float,
+                                   block_prior: Optional[torch.Tensor] = None, prior_alpha: float = 1.0,
+                                   prior_eps: float = 0.1):
+    """Drop-in for `_energy_expanded_active_blocks` (RRD:144-176): top-n_keep blocks by energy
+    (optional prior), grown to the first rank whose cumulative energy reaches energy_keep of
+    the total.  Returns (ascending int32 ids, kept energy ratio, kept density) like the
+    reference, which synchronises for the count."""
+    x3 = x.reshape(x.shape[0], 1, x.shape[-1]) if x.dim() == 2 else x
+    if x3.shape[1] != 1 or density >= 1.0:
+        return None, 1.0, 1.0
+    if int(block_k) != BLOCK_K:
+        raise ValueError(f"block_k must be {BLOCK_K}")
+    nb = x3.shape[-1] // BLOCK_K
+    nk = n_keep_for_density(density, nb)
+    idx, cnt, ratio = select_topk(x3, nk, score="energy", block_prior=block_prior, prior_alpha=prior_alpha,
+                                  prior_eps=prior_eps, energy_keep=float(energy_keep), workspace_prefix="select_ref")
+    keep = int(cnt.item())
+    return idx[:keep], float(ratio.item()), float(keep / nb)
+
+
 def select_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, k: int, cache_prefix: str = "sel_gemm",
                        plan=None, idx_out: Optional[torch.Tensor] = None,
                        count_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -736,6 +736,200 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   }
 }
 
+
+// Reference scoring rules (scripts/bench_roundrobin_e2e_decode.py:90-176) on the device, in
+// fp64: per block j over its 64 channels, with b over the bt rows,
+//   L2 mean       e2_j = mean_b sqrt(sum_c x^2)                       (RRD:100)
+//   energy        e_j  = mean_b sum_c x^2 [* scale_c]                 (RRD:103-105, 131)
+// optionally times max(prior_j + eps, 1e-6)^alpha (RRD:106-112).  Blocks are floor(K/64), as
+// there.  Ranking is (score desc, id asc); with an energy budget the kept count grows from k to
+// the first rank whose cumulative (unscaled) energy reaches budget * total (RRD:155-176).
+struct SelScoreParams {
+  const void* x;
+  int64_t ldx;
+  const float* prior;
+  const float* scale;
+  double* scores;
+  double* energy;
+  uint32_t* cnt;
+  int32_t* idx_out;
+  int32_t* na_out;
+  float* ratio_out;
+  float alpha, eps, energy_keep;
+  int32_t bt, K, nb, k, mode;
+};
+
+template <typename T>
+__device__ __forceinline__ float elem_to_float(uint32_t bits16);
+template <>
+__device__ __forceinline__ float elem_to_float<_Float16>(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+template <>
+__device__ __forceinline__ float elem_to_float<__bf16>(uint32_t b) {
+  return __builtin_bit_cast(float, b << 16);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void bsg_select_score_kernel(SelScoreParams p) {
+  __shared__ double s_sc[BSG_MAX_NBLK];
+  __shared__ double s_en[BSG_MAX_NBLK];
+  __shared__ int s_order[BSG_MAX_NBLK];
+  __shared__ uint8_t s_sel[BSG_MAX_NBLK];
+  __shared__ double s_part[3][4];
+  __shared__ double s_csum[256];
+  __shared__ double s_total;
+  __shared__ int s_scan[4];
+  __shared__ int s_last, s_keep, s_first;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = blockIdx.x;
+
+  // Thread gi: row gi / 8, channels 64j + 8(gi % 8) .. +7; the 8 threads of a row are
+  // adjacent lanes, so a row's sum of squares is a 3-step butterfly.
+  double a_l2 = 0.0, a_e = 0.0, a_es = 0.0;
+  const int rows = p.bt;
+  for (int r0 = 0; r0 < rows; r0 += 32) {
+    const int row = r0 + (tid >> 3);
+    const int c0 = 64 * j + 8 * (tid & 7);
+    double sq = 0.0, sqs = 0.0;
+    if (row < rows) {
+      const u32x4 v = *(const u32x4*)((const uint16_t*)p.x + (size_t)row * (size_t)p.ldx + c0);
+      const uint32_t h[8] = {v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16,
+                             v.z & 0xffffu, v.z >> 16, v.w & 0xffffu, v.w >> 16};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const double f = (double)elem_to_float<T>(h[e]);
+        sq += f * f;
+        if (p.scale) sqs += f * f * (double)p.scale[c0 + e];
+      }
+    }
+    sq += __shfl_xor(sq, 1, 64);
+    sq += __shfl_xor(sq, 2, 64);
+    sq += __shfl_xor(sq, 4, 64);
+    sqs += __shfl_xor(sqs, 1, 64);
+    sqs += __shfl_xor(sqs, 2, 64);
+    sqs += __shfl_xor(sqs, 4, 64);
+    if ((tid & 7) == 0 && row < rows) {
+      a_l2 += sqrt(sq);
+      a_e += sq;
+      a_es += sqs;
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    a_l2 += __shfl_xor(a_l2, d, 64);
+    a_e += __shfl_xor(a_e, d, 64);
+    a_es += __shfl_xor(a_es, d, 64);
+  }
+  if (lane == 0) {
+    s_part[0][w] = a_l2;
+    s_part[1][w] = a_e;
+    s_part[2][w] = a_es;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const double inv = 1.0 / (double)rows;
+    const double l2 = (((s_part[0][0] + s_part[0][1]) + s_part[0][2]) + s_part[0][3]) * inv;
+    const double en = (((s_part[1][0] + s_part[1][1]) + s_part[1][2]) + s_part[1][3]) * inv;
+    const double es = (((s_part[2][0] + s_part[2][1]) + s_part[2][2]) + s_part[2][3]) * inv;
+    double sc = p.mode == BSG_SCORE_L2_MEAN ? l2 : (p.scale ? es : en);
+    if (p.prior) {
+      const double pr = (double)p.prior[j] + (double)p.eps;
+      sc *= pow(pr > 1e-6 ? pr : 1e-6, (double)p.alpha);
+    }
+    // Score and energy out through agent-scope stores; once they have completed, count the
+    // arrival (the last work-group reads them with agent-scope loads).
+    __hip_atomic_store(&p.scores[j], sc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&p.energy[j], en, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    const unsigned prev = __hip_atomic_fetch_add(p.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(p.nb - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  const int nb = p.nb;
+  for (int i = tid; i < nb; i += 256) {
+    s_sc[i] = __hip_atomic_load(&p.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_en[i] = __hip_atomic_load(&p.energy[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  // rank of every block; order[rank] = block
+  for (int jj = tid; jj < nb; jj += 256) {
+    const double sj = s_sc[jj];
+    int rank = 0;
+    for (int i = 0; i < nb; ++i) {
+      const double si = s_sc[i];
+      rank += (si > sj) || (si == sj && i < jj);
+    }
+    s_order[rank] = jj;
+  }
+  const int k0 = p.k < nb ? p.k : nb;
+  if (tid == 0) {
+    s_keep = k0;
+    s_first = nb;
+  }
+  for (int i = tid; i < nb; i += 256) s_sel[i] = 0;
+  __syncthreads();  // s_sc is free again: it holds the cumulative energy by rank from here on
+  if (p.energy_keep > 0.f || p.ratio_out) {
+    // Cumulative energy in rank order: each thread sums a contiguous run of ranks, the run
+    // totals are scanned in thread order, then each run is walked again.
+    const int per = (nb + 255) / 256;
+    const int beg = tid * per < nb ? tid * per : nb;
+    const int end = beg + per < nb ? beg + per : nb;
+    double run = 0.0;
+    for (int r = beg; r < end; ++r) run += s_en[s_order[r]];
+    s_csum[tid] = run;
+    __syncthreads();
+    if (tid == 0) {
+      double acc = 0.0;
+      for (int t = 0; t < 256; ++t) {
+        const double v = s_csum[t];
+        s_csum[t] = acc;
+        acc += v;
+      }
+      s_total = acc;
+    }
+    __syncthreads();
+    const double thr = (double)p.energy_keep * (s_total > 1e-12 ? s_total : 1e-12);
+    double cum = s_csum[tid];
+    int first = nb;
+    for (int r = beg; r < end; ++r) {
+      cum += s_en[s_order[r]];
+      s_sc[r] = cum;
+      if (first == nb && cum >= thr) first = r;
+    }
+    if (first < nb) atomicMin(&s_first, first);
+    __syncthreads();
+    if (tid == 0) {
+      const double total = s_total > 1e-12 ? s_total : 1e-12;
+      int keep = k0;
+      if (p.energy_keep > 0.f && k0 > 0 && s_sc[k0 - 1] / total < (double)p.energy_keep) {
+        keep = s_first + 1;
+        keep = keep < k0 ? k0 : (keep > nb ? nb : keep);
+      }
+      s_keep = keep;
+      if (p.ratio_out) *p.ratio_out = keep > 0 ? (float)(s_sc[keep - 1] / total) : 0.f;
+    }
+    __syncthreads();
+  }
+  const int keep = s_keep;
+  for (int r = tid; r < keep; r += 256) s_sel[s_order[r]] = 1;
+  __syncthreads();
+  const int per = (nb + 255) / 256;
+  const int beg = tid * per < nb ? tid * per : nb;
+  const int end = beg + per < nb ? beg + per : nb;
+  int c = 0;
+  for (int jj = beg; jj < end; ++jj) c += s_sel[jj];
+  int total = 0;
+  int o = wg_exclusive_scan<256>(c, s_scan, &total);
+  for (int jj = beg; jj < end; ++jj)
+    if (s_sel[jj]) p.idx_out[o++] = jj;
+  if (tid == 0) {
+    *p.na_out = keep;
+    __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 // Pack W (logical [N,K], element strides sn/sk) into the tiled K-major layout.
 // One thread per 8-element (16-byte) group of the packed slab.
 __global__ __launch_bounds__(256) void bsg_pack_kernel(const uint16_t* __restrict__ w, int64_t N,
@@ -1237,7 +1431,7 @@ int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K, const void
 
 int64_t bsg_select_workspace_bytes(int64_t K) {
   if (K <= 0) return -1;
-  return cdiv(256 + cdiv(K, BSG_BLOCK_K) * 8, 256) * 256;
+  return cdiv(256 + cdiv(K, BSG_BLOCK_K) * 16, 256) * 256;
 }
 
 int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
@@ -1270,6 +1464,63 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
   hipLaunchKernelGGL(bsg_select_l1_kernel, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 launch");
+  return BSG_OK;
+}
+
+int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
+                    int32_t* idx_out, int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
+  const bsg_select_opts o = opts ? *opts : bsg_select_opts{BSG_SCORE_L1, 0.f, nullptr, 1.f, 0.1f, nullptr, nullptr};
+  if (o.score == BSG_SCORE_L1) {
+    if (o.energy_keep != 0.f || o.block_prior || o.channel_scale || o.ratio_out)
+      return fail(BSG_ERR_UNSUPPORTED, "select: the exact L1 score takes no prior, scale or energy budget");
+    return bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
+  }
+  if (o.score != BSG_SCORE_L2_MEAN && o.score != BSG_SCORE_ENERGY)
+    return fail(BSG_ERR_UNSUPPORTED, "select: score=%d (0 = L1, 1 = L2 mean, 2 = energy)", o.score);
+  if (dtype != BSG_F16 && dtype != BSG_BF16) return fail(BSG_ERR_DTYPE, "select: dtype=%d", dtype);
+  if (bt <= 0 || K < BSG_BLOCK_K)
+    return fail(BSG_ERR_ARG, "select: bt=%lld K=%lld (scored blocks are floor(K/64) >= 1)", (long long)bt,
+                (long long)K);
+  const int64_t nb = K / BSG_BLOCK_K;
+  if (cdiv(K, BSG_BLOCK_K) > BSG_MAX_NBLK) return fail(BSG_ERR_UNSUPPORTED, "select: K=%lld too large", (long long)K);
+  if (k < 0) return fail(BSG_ERR_ARG, "select: k=%d", k);
+  if (!(o.energy_keep >= 0.f && o.energy_keep <= 1.f))
+    return fail(BSG_ERR_ARG, "select: energy_keep=%g outside [0, 1]", (double)o.energy_keep);
+  if (o.channel_scale && o.score != BSG_SCORE_ENERGY)
+    return fail(BSG_ERR_ARG, "select: channel_scale applies to the energy score only");
+  if (!x || !idx_out || !na_out) return fail(BSG_ERR_ARG, "select: null pointer");
+  if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || !aligned16(x))
+    return fail(BSG_ERR_ALIGN, "select: x must be 16-byte aligned, K %% 8 == 0, ldx %% 8 == 0");
+  if (bt > (1 << 24)) return fail(BSG_ERR_UNSUPPORTED, "select: bt too large");
+  const int64_t need = bsg_select_workspace_bytes(K);
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
+                (long long)need);
+  SelScoreParams p;
+  p.x = x;
+  p.ldx = ldx;
+  p.prior = o.block_prior;
+  p.scale = o.channel_scale;
+  p.cnt = (uint32_t*)ws;
+  p.scores = (double*)((char*)ws + 256);
+  p.energy = p.scores + cdiv(K, BSG_BLOCK_K);
+  p.idx_out = idx_out;
+  p.na_out = na_out;
+  p.ratio_out = o.ratio_out;
+  p.alpha = o.prior_alpha;
+  p.eps = o.prior_eps;
+  p.energy_keep = o.energy_keep;
+  p.bt = (int32_t)bt;
+  p.K = (int32_t)K;
+  p.nb = (int32_t)nb;
+  p.k = k;
+  p.mode = o.score;
+  if (dtype == BSG_F16)
+    hipLaunchKernelGGL(bsg_select_score_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(bsg_select_score_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk launch");
   return BSG_OK;
 }
 
