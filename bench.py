@@ -3,10 +3,10 @@
 
 Workload: Llama-2-7B down_proj, B=16, K=11008 (172 blocks of 64),
 N=4096, fp16, sweeping block sparsity {0, 0.25, 0.5, 0.638, 0.8}; the 0% point runs the same
-kernel with every block active (the in-run dense baseline).  One "step" = every sweep point
-once, where a point is a hipGraph of R back-to-back GEMM launches, each on a different copy
-of the packed weight (R copies span >= 1 GiB, so the 256 MB Infinity Cache cannot serve a
-repeat and the bytes really come from HBM).
+kernel with every block active (the in-run dense baseline).  One "step" = one replay of a
+hipGraph holding every sweep point's R back-to-back GEMM launches, each on a different copy of
+the packed weight (R copies span >= 1 GiB, so the 256 MB Infinity Cache cannot serve a repeat
+and the bytes really come from HBM).  Per-point µs/GEMM come from each point's own graph.
 
 value  = active-weight bytes of all GEMMs in the timed steps / timed seconds (GB/s)
 roofline = the s=0.5 sparse GEMM (86/172 blocks): algorithmic bytes na*64*N*2 per launch over
@@ -126,36 +126,59 @@ class Point:
         return orc.rel_frobenius(y, ref), orc.within_tolerance(y, ref)
 
 
-def time_points(points, steps, warmup):
-    """Warm-up, then exactly `steps` steps (each point's graph replayed once per step), with a
-    per-point HIP-event pair on the launch stream around every replay."""
+def capture_step(points):
+    """One hipGraph holding a whole step: every point's R rotated launches, back to back."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for p in points:
+            for i in range(p.copies):
+                p.launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for p in points:
+            for i in range(p.copies):
+                p.launch(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_points(points, step_graph, steps, warmup, reps=10):
+    """Warm-up, then exactly `steps` replays of the step graph between a synchronize + event
+    pair on each side (the timed region); then each point's own graph, `reps` replays with a
+    HIP-event pair on the launch stream around each, for the per-GEMM times."""
     import torch
 
     for _ in range(warmup):
-        for p in points:
-            p.graph.replay()
-    torch.cuda.synchronize()
-    ev = {p.name: [] for p in points}
+        step_graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start_all = torch.cuda.Event(enable_timing=True)
     end_all = torch.cuda.Event(enable_timing=True)
     start_all.record()
     for _ in range(steps):
-        for p in points:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            p.graph.replay()
-            b.record()
-            ev[p.name].append((a, b))
+        step_graph.replay()
     end_all.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start_all.elapsed_time(end_all)
     per = {}
     for p in points:
-        us = [a.elapsed_time(b) * 1000.0 / p.copies for a, b in ev[p.name]]
+        p.graph.replay()
+        torch.cuda.synchronize()
+        us = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            p.graph.replay()
+            b.record()
+            b.synchronize()
+            us.append(a.elapsed_time(b) * 1000.0 / p.copies)
         per[p.name] = (statistics.median(us), statistics.mean(us))
     return total_ms, wall, per
 
@@ -248,6 +271,33 @@ def torch_mm_us(point, reps=5):
         ts.append(a.elapsed_time(b) * 1000.0 / len(ws))
     del g, ws
     return statistics.median(ts)
+
+
+def read_calibration_us(point, reps=5):
+    """Practical HBM read time of one launch streaming the point's active-weight bytes: the
+    library's read-rate calibration kernel (the GEMM's weight-load pattern, no compute),
+    rotated over the same weight copies and timed the same way."""
+    import torch
+
+    import bsa_mi355x as bsa
+
+    lib = bsa.load()
+    nbytes = point.active_bytes // 1024 * 1024
+    sink = torch.zeros(4, dtype=torch.int32, device=point.x.device)
+
+    def launch(i):
+        def f():
+            rc = lib.bsg_read_calibrate(point.packed[i].data_ptr(), nbytes, sink.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(lib.bsg_last_error().decode())
+        return f
+
+    med, _ = _graph_time([launch(i) for i in range(point.copies)], reps)
+    return med / point.copies
+
+
+KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel"}
 
 
 def _graph_time(fns, reps, warmup=2):
@@ -464,9 +514,10 @@ def main():
     log("parity ok on every point")
     for p in points:
         p.capture()
+    step_graph = capture_step(points)
     log("graphs captured")
 
-    total_ms, wall, per = time_points(points, args.steps, args.warmup)
+    total_ms, wall, per = time_points(points, step_graph, args.steps, args.warmup)
     step_bytes = sum(p.active_bytes * p.copies for p in points)
     value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
     log(f"timed {args.steps} steps in {total_ms:.2f} ms (host wall {wall * 1e3:.1f} ms)")
@@ -500,8 +551,16 @@ def main():
     achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-                "kernel": "bsg_gemm_kernel", "point": focus, "avg_launch_us": round(f_mean, 3),
-                "bytes_per_launch": fp.active_bytes}
+                "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
+                "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes}
+    if not args.only:
+        rd = read_calibration_us(fp)
+        roofline["practical_read"] = {
+            "us_per_launch": round(rd, 3), "GBps": round(fp.active_bytes / (rd * 1e-6) / 1e9, 1),
+            "frac_of_it": round(rd / f_mean, 4),
+            "what": "bsg_read_calibrate streaming the same bytes per launch (weight-load pattern, no compute), "
+                    "same rotation and timing"}
+        log(f"practical read of {fp.active_bytes / 1e6:.2f} MB: {rd:.2f} us ({roofline['practical_read']['GBps']} GB/s)")
     dense_pt = next((p for p in points if p.dense and p.name.startswith("down_b16")), None)
     if dense_pt is not None and not args.only:
         mm = torch_mm_us(dense_pt)

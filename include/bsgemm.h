@@ -186,6 +186,13 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
                     void* y, int64_t ldy, int dtype,
                     void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
+/* Read-rate calibration; no counterpart in the reference.  Streams `bytes` (a multiple of
+ * 1024) from src with the GEMM's weight-load pattern (non-temporal 1 KiB wave loads, 8 waves
+ * per compute unit) and writes sink[0] only if the data folds to a fixed constant.  Its
+ * duration is the practical HBM read time of a launch of that size, the context for a
+ * GEMM's fraction of the 8 TB/s peak. */
+int bsg_read_calibrate(const void* src, int64_t bytes, void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,6 +109,7 @@ SIGNATURES = {
                                _i64, _vp]),
     "bsg_select_gemm": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _i64,
                                _pplan, _vp]),
+    "bsg_read_calibrate": (_int, [_vp, _i64, _vp, _vp]),
 }
 
 _lock = threading.Lock()

@@ -930,6 +930,38 @@ __global__ __launch_bounds__(256) void bsg_select_score_kernel(SelScoreParams p)
     __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+// Read-rate calibration (no counterpart in the reference): streams `bytes` from src with the
+// access pattern of the GEMM's weight stream (one 1 KiB wave-load per 16-byte lane slice,
+// non-temporal, DEPTH = 4 in flight, each wave walking its own contiguous run), and writes only
+// if the data XOR-folds to a value the caller names, so the loads cannot be dropped.  It gives
+// the practical HBM read time of a launch of the same size on this device.
+__global__ __launch_bounds__(256) void bsg_read_kernel(const char* __restrict__ src, int64_t n1k, uint32_t magic,
+                                                       uint32_t* __restrict__ sink) {
+  constexpr int DEPTH = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t per = (n1k + nw - 1) / nw;
+  const int64_t beg = wv * per;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  u32x4 v[DEPTH];
+  auto load = [&](int64_t i) -> u32x4 {
+    const int64_t b = beg + i;
+    const bool ok = i < per && b < n1k;
+    return ld16_stream(make_rsrc(src + (ok ? b : 0) * 1024, ok ? 1024 : 0), lane * 16);
+  };
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) v[d] = load(d);
+  for (int64_t i0 = 0; i0 < per; i0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      acc ^= v[d];
+      v[d] = load(i0 + d + DEPTH);
+    }
+  }
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == magic) sink[0] = 1u;
+}
+
 // Pack W (logical [N,K], element strides sn/sk) into the tiled K-major layout.
 // One thread per 8-element (16-byte) group of the packed slab.
 __global__ __launch_bounds__(256) void bsg_pack_kernel(const uint16_t* __restrict__ w, int64_t N,
@@ -1521,6 +1553,22 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
     hipLaunchKernelGGL(bsg_select_score_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bsg_select_topk launch");
+  return BSG_OK;
+}
+
+int bsg_read_calibrate(const void* src, int64_t bytes, void* sink, void* stream) {
+  if (!src || !sink || bytes < 1024 || bytes % 1024 != 0)
+    return fail(BSG_ERR_ARG, "read_calibrate: bytes=%lld (a positive multiple of 1024) and non-null pointers",
+                (long long)bytes);
+  if (!aligned16(src)) return fail(BSG_ERR_ALIGN, "read_calibrate: src must be 16-byte aligned");
+  const int64_t n1k = bytes / 1024;
+  const int cu = device_cu_count();
+  int64_t groups = 2 * (int64_t)cu;  // 8 waves per compute unit
+  if (groups * 4 > n1k) groups = (n1k + 3) / 4;
+  hipLaunchKernelGGL(bsg_read_kernel, dim3((unsigned)groups), dim3(256), 0, (hipStream_t)stream, (const char*)src,
+                     n1k, 0x9E3779B9u, (uint32_t*)sink);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_read_calibrate launch");
   return BSG_OK;
 }
 
