@@ -13,7 +13,7 @@ roofline = the s=0.5 sparse GEMM (86/172 blocks): algorithmic bytes na*64*N*2 pe
            the average launch duration from HIP events around its graph replays.
 cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul) on the s=0.5 point.
 
-    python bench.py [--steps K] [--warmup W] [--workload down_sweep|llama|fused]
+    python bench.py [--steps K] [--warmup W] [--workload down_sweep|llama|fused|decode|perstep]
 """
 from __future__ import annotations
 
@@ -47,7 +47,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="down_sweep", choices=["down_sweep", "llama", "fused", "decode"])
+    ap.add_argument("--workload", default="down_sweep", choices=["down_sweep", "llama", "fused", "decode", "perstep"])
+    ap.add_argument("--batches", default=None, help="perstep workload: batch sizes (default: all six)")
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -450,6 +451,134 @@ def run_decode(args, dev):
     print(json.dumps(line), flush=True)
 
 
+PERSTEP_FIXTURE = os.path.join(ROOT, "tests", "golden", "perstep_smaps.npz")
+PERSTEP_SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
+PERSTEP_PROJ_SHAPE = ["qkvo", "qkvo", "qkvo", "qkvo", "gate_up", "gate_up", "down"]
+
+
+class ShapePool:
+    """Packed-weight copies (>= 1 GiB) of one projection shape, plus [K,N] copies for
+    torch.mm, shared by every density and batch of the per-step replay."""
+
+    def __init__(self, name, k, n, dev, seed):
+        import numpy as np
+        import torch
+
+        import bsa_mi355x as bsa
+
+        self.name, self.k, self.n = name, k, n
+        self.nblk = (k + 63) // 64
+        rng = np.random.default_rng(seed)
+        w_kn = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float16)
+        self.w_kn_np = w_kn
+        w0 = torch.from_numpy(w_kn).to(dev)
+        p0 = bsa.pack_weight(w0, layout="kn")
+        self.copies = max(1, math.ceil(ROTATE_BYTES / (p0.numel() * 2)))
+        self.packed = [p0] + [p0.clone() for _ in range(self.copies - 1)]
+        self.w_kn = [w0] + [w0.clone() for _ in range(self.copies - 1)]
+
+
+def run_perstep(args, dev):
+    """Oracle-map replay (the reference's headline,
+    scripts/bench_perstep_actual_kernel_speedup.py): for each batch size, every group-step's
+    S-map of 7 projections x 32 layers (tests/golden/perstep_smaps.npz, from the reference's
+    results/oracle/perstep_batch_sweep.json) gives 224 GEMMs with density 1 - S and
+    floor(density * nblk) random active blocks (BPS:84-87).  Each distinct (shape, density) is
+    timed once (the reference's unique-case method, BPS:148-172) with this build's sparse kernel,
+    its dense variant and hipBLASLt (torch.mm), every one rotated over >= 1 GiB of weight
+    copies; a step's speedup is sum(dense) / sum(sparse) over its 224 GEMMs, averaged over the
+    55 group-steps of a batch size, next to the reference's A100X numbers for the same maps."""
+    import numpy as np
+    import torch
+
+    import bsa_mi355x as bsa
+    from oracle import bsg_oracle as orc
+
+    fx = np.load(PERSTEP_FIXTURE, allow_pickle=False)
+    batches = [int(b) for b in (args.batches.split(",") if args.batches else fx["ref_batch"])]
+    pools = {name: ShapePool(name, k, n, dev, 1234 + i) for i, (name, (k, n)) in enumerate(PERSTEP_SHAPES.items())}
+    log("perstep: weight pools " + ", ".join(f"{p.name} x{p.copies}" for p in pools.values()))
+    rng = np.random.default_rng(1234)
+    reps = max(3, min(args.steps, 10))
+
+    def timed(fns):
+        return _graph_time(fns, reps)[0] / len(fns)
+
+    results = []
+    total_bytes = 0.0
+    total_us = 0.0
+    for bt in batches:
+        sel = np.nonzero(fx["batch"] == bt)[0]
+        maps = fx["smap_tenths"][sel]  # [steps, 7, 32] sparsity in tenths
+        cases = sorted({(PERSTEP_PROJ_SHAPE[pi], 10 - int(t)) for m in maps for pi in range(7) for t in m[pi]})
+        x = {name: torch.randn(bt, p.k, generator=torch.Generator().manual_seed(bt), dtype=torch.float32)
+             .to(torch.float16).to(dev) for name, p in pools.items()}
+        y = {name: torch.empty(bt, p.n, dtype=torch.float16, device=dev) for name, p in pools.items()}
+        dense_us, mm_us = {}, {}
+        for name, p in pools.items():
+            pl = bsa.resolve_plan(bt, p.n, p.nblk, p.nblk, dev, None, dense=True)
+            dense_us[name] = timed([(lambda i=i: bsa.gemm_packed(x[name], p.packed[i], p.n, None, y[name], plan=pl,
+                                                                  workspace_prefix=f"ps_dense_{name}"))
+                                    for i in range(p.copies)])
+            mm_us[name] = timed([(lambda i=i: torch.mm(x[name], p.w_kn[i], out=y[name])) for i in range(p.copies)])
+        sparse_us = {}
+        for name, tenths in cases:
+            p = pools[name]
+            na = max(1, min(p.nblk, int(math.floor(tenths / 10.0 * p.nblk))))
+            idx = torch.from_numpy(np.sort(rng.choice(p.nblk, na, replace=False)).astype(np.int32)).to(dev)
+            pl = bsa.resolve_plan(bt, p.n, p.nblk, na, dev, None)
+            fns = [(lambda i=i: bsa.gemm_packed(x[name], p.packed[i], p.n, idx, y[name], plan=pl,
+                                                workspace_prefix=f"ps_{name}")) for i in range(p.copies)]
+            fns[0]()
+            torch.cuda.synchronize()
+            if tenths in (1, 5, 9):  # spot parity on three densities per shape
+                ref = orc.gemm_ref(x[name].float().cpu().numpy(), np.ascontiguousarray(p.w_kn_np.T),
+                                   idx.cpu().numpy())
+                if not orc.within_tolerance(y[name].float().cpu().numpy(), ref):
+                    raise SystemExit(f"perstep B={bt} {name} density {tenths / 10}: output outside tolerance")
+            us = timed(fns)
+            sparse_us[(name, tenths)] = (us, na)
+            total_bytes += na * 64 * p.n * 2
+            total_us += us
+        step_own, step_mm = [], []
+        for m in maps:
+            d_sum = m_sum = s_sum = 0.0
+            for pi in range(7):
+                name = PERSTEP_PROJ_SHAPE[pi]
+                for t in m[pi]:
+                    us, _ = sparse_us[(name, 10 - int(t))]
+                    s_sum += us
+                    d_sum += dense_us[name]
+                    m_sum += mm_us[name]
+            step_own.append(d_sum / s_sum)
+            step_mm.append(m_sum / s_sum)
+        ref_i = list(fx["ref_batch"]).index(bt) if bt in list(fx["ref_batch"]) else None
+        row = {"B": bt, "group_steps": int(len(sel)), "mean_sparsity": round(float(fx["mean_sparsity"][sel].mean()), 4),
+               "unique_cases": len(cases),
+               "speedup_vs_own_dense": round(float(np.mean(step_own)), 3),
+               "speedup_vs_hipblaslt": round(float(np.mean(step_mm)), 3),
+               "reference_a100x_speedup_vs_cublas": (round(float(fx["ref_batch_speedup"][ref_i]), 3)
+                                                     if ref_i is not None else None),
+               "dense_us": {k: round(v, 2) for k, v in dense_us.items()},
+               "hipblaslt_us": {k: round(v, 2) for k, v in mm_us.items()},
+               "sparse_us_step_mean": round(float(np.mean([sum(sparse_us[(PERSTEP_PROJ_SHAPE[pi], 10 - int(t))][0]
+                                                               for pi in range(7) for t in m[pi]) for m in maps])), 1)}
+        results.append(row)
+        log(json.dumps(row))
+    line = {
+        "metric": METRIC, "value": round(total_bytes / (total_us * 1e-6) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps, "warmup": 2, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16",
+        "data": "reference S-maps (results/oracle/perstep_batch_sweep.json via tests/golden/perstep_smaps.npz); "
+                "W~N(0,0.02), X~N(0,1) synthetic; random masks floor(density*nblk); weights rotated over >=1 GiB",
+        "config": {"workload": "oracle-map replay of the 224-GEMM decode step (7 projections x 32 layers), "
+                               "B in " + ",".join(map(str, batches)) + " (the reference's headline speedup table)",
+                   "value_is": "active-weight bytes / time over every distinct timed sparse case"},
+        "perstep": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -494,6 +623,9 @@ def main():
         focus = "gate_up_b64_s520"
     elif args.workload == "fused":
         run_fused(args, dev)
+        return
+    elif args.workload == "perstep":
+        run_perstep(args, dev)
         return
     else:
         run_decode(args, dev)

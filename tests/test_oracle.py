@@ -220,3 +220,17 @@ def test_scored_selector_ties_and_prior():
     assert np.array_equal(ids, [2, 3])
     ids, _, _ = orc.select_scored_ref(x, 1, "energy", prior=np.array([-5, 0, 0, 0], np.float32), alpha=2.0, eps=0.1)
     assert np.array_equal(ids, [1])  # prior clamped to 1e-6 for block 0; ties among 1..3 -> 1
+
+
+def test_perstep_fixture_matches_reference_summaries():
+    """The S-map fixture (tests/golden/make_perstep_fixture.py, from the reference's result
+    files) decodes to the mean sparsity the reference recorded for each group-step, and the
+    reference's per-batch speedups are the means of its per-step ones."""
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "perstep_smaps.npz"), allow_pickle=False)
+    maps = f["smap_tenths"].astype(np.float64) / 10.0
+    assert maps.shape == (330, 7, 32) and maps.max() <= 0.9
+    assert np.abs(maps.reshape(330, -1).mean(axis=1) - f["mean_sparsity"]).max() < 1e-12
+    for b, s in zip(f["ref_batch"], f["ref_batch_speedup"]):
+        sel = f["batch"] == b
+        assert sel.sum() == 55 and abs(f["ref_step_speedup"][sel].mean() - s) < 1e-12
+    assert [round(float(v), 3) for v in f["ref_batch_speedup"]] == [1.948, 1.945, 1.761, 1.602, 1.405, 1.203]

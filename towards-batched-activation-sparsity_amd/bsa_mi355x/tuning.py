@@ -155,7 +155,7 @@ def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
             if rows == fma_rows:
                 out.append(Plan(1, cols, waves, depth, rows, kind))
             continue
-        if rows != rb:
+        if rows != rb and not (rb == 32 and rows == 64):  # 32-row batches also try 64-row tiles
             continue
         for sk in (1, 2, 3, 4, 6, 8):
             if sk * (waves if kind == 1 else 1) > max(na, 1):
@@ -220,7 +220,7 @@ class _Case:
 
 def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densities: Sequence[float],
          out_table: str = TABLE_PATH, lookup_dir: Optional[str] = None, rotate_bytes: int = 1 << 30,
-         seed: int = 1234, log=print) -> List[dict]:
+         seed: int = 1234, log=print, merge_from: Optional[str] = None) -> List[dict]:
     """Profile every candidate plan for shape x batch x density; write the flat table (and the
     per-batch reference-layout lookups when lookup_dir is given).  Active blocks per density:
     max(1, floor(density * nblk)) as in scripts/profile_kernel_configs.py:111."""
@@ -265,6 +265,12 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
             del case
             torch.cuda.empty_cache()
     meta = {"device": torch.cuda.get_device_name(dev), "rotate_bytes": rotate_bytes, "seed": seed}
+    if merge_from:
+        # keep the other (shape, batch) entries of an existing table
+        tuned = {(e["shape"], e["bt"]) for e in entries}
+        with open(merge_from) as f:
+            old = json.load(f)
+        entries = [e for e in old.get("entries", []) if (e["shape"], e["bt"]) not in tuned] + entries
     with open(out_table, "w") as f:
         json.dump({"meta": meta, "entries": entries}, f, indent=1)
     if lookup_dir:
@@ -283,10 +289,13 @@ def main(argv: Optional[Iterable[str]] = None) -> None:
     ap.add_argument("--densities", default="0.1,0.2,0.3,0.4,0.5,0.6,0.7,0.8,0.9")
     ap.add_argument("--out", default=TABLE_PATH)
     ap.add_argument("--lookup-dir", default=None)
+    ap.add_argument("--merge", action="store_true",
+                    help="keep the other (shape, batch) entries of the shipped table in the output")
     args = ap.parse_args(list(argv) if argv is not None else None)
     shapes = {s: LLAMA2_7B_SHAPES[s] for s in args.shapes.split(",")}
     tune(shapes, [int(b) for b in args.batch_sizes.split(",")], [float(d) for d in args.densities.split(",")],
-         out_table=args.out, lookup_dir=args.lookup_dir, log=lambda m: print(m, flush=True))
+         out_table=args.out, lookup_dir=args.lookup_dir, log=lambda m: print(m, flush=True),
+         merge_from=TABLE_PATH if args.merge else None)
 
 
 if __name__ == "__main__":
