@@ -60,7 +60,9 @@ enum bsg_status {
  *                     share each block's activation tile through LDS (work-group columns =
  *                     cols_per_wave * waves_per_group); 3 = fp32 dot products instead of MFMA
  *                     for 1-8 rows, the work-group's activations staged in LDS once, split_k 1,
- *                     only when named (automatic plans take kinds 1-2)
+ *                     only when named (automatic plans take kinds 1-2); 4 = as 2, with the waves
+ *                     split over columns and over the two 32-channel halves of every block (two
+ *                     waves per SIMD; work-group columns = cols_per_wave * waves_per_group / 2)
  * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
  * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
 typedef struct bsg_plan {

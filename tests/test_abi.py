@@ -71,7 +71,9 @@ def test_plan_resolve_rejects():
     assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 4))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
+    # kind 4 pairs the waves over channel halves: one wave has no partner
+    assert _resolve(64, 4096, 64, 1, plan=_lib.Plan(0, 16, 1, 4, 64, 4))[0] == _lib.BSG_ERR_UNSUPPORTED
     # kind 3: no split-K, 1-8 rows, and its activation staging must hold the list
     assert _resolve(4, 4096, 64, 8, plan=_lib.Plan(2, 0, 0, 0, 0, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(4, 4096, 64, 8, plan=_lib.Plan(0, 0, 0, 0, 16, 3))[0] == _lib.BSG_ERR_UNSUPPORTED
@@ -87,6 +89,8 @@ def test_workspace_bytes():
     p = _lib.Plan(4, 32, 4, 4, 16, 1)
     tiles = 4096 // 32
     assert lib.bsg_gemm_workspace_bytes(16, 4096, ctypes.byref(p)) == 512 + tiles * 4 * 2 * 64 * 16
+    p = _lib.Plan(2, 16, 8, 4, 64, 4)  # kind 4: 8 waves = 4 column groups x 2 channel halves
+    assert lib.bsg_gemm_workspace_bytes(64, 4096, ctypes.byref(p)) == 256 + 64 * 2 * (4 * 4) * 64 * 16
     p = _lib.Plan(2, 16, 4, 4, 64, 2)  # kind 2: a work-group covers 16 * 4 columns
     tiles = 4096 // 64
     assert lib.bsg_gemm_workspace_bytes(64, 4096, ctypes.byref(p)) == 256 + tiles * 2 * (4 * 4) * 64 * 16

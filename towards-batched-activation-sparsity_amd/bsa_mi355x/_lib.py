@@ -63,6 +63,15 @@ class Plan(ctypes.Structure):
     def as_tuple(self):
         return (self.split_k, self.cols_per_wave, self.waves_per_group, self.depth, self.rows_per_group, self.kind)
 
+    def group_cols(self) -> int:
+        """Output columns one work-group covers: waves split columns in kind 2, column groups
+        x channel halves in kind 4, the block list in kinds 1 and 3."""
+        if self.kind == 2:
+            return self.cols_per_wave * self.waves_per_group
+        if self.kind == 4:
+            return self.cols_per_wave * (self.waves_per_group // 2)
+        return self.cols_per_wave
+
     def __repr__(self) -> str:
         return ("Plan(split_k=%d, cols_per_wave=%d, waves_per_group=%d, depth=%d, rows_per_group=%d, kind=%d)"
                 % self.as_tuple())

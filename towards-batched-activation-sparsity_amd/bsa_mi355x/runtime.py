@@ -235,8 +235,7 @@ class _KernelHandle:
         p = self.last_plan
         if p is None:
             return None
-        cols = p.cols_per_wave * (p.waves_per_group if p.kind == 2 else 1)
-        return TileConfig({"BLOCK_B": p.rows_per_group, "BLOCK_N": cols}, num_warps=p.waves_per_group,
+        return TileConfig({"BLOCK_B": p.rows_per_group, "BLOCK_N": p.group_cols()}, num_warps=p.waves_per_group,
                           num_stages=p.depth, split_k=p.split_k, kind=p.kind)
 
 
@@ -509,7 +508,7 @@ def dense_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, cache_p
 def kernel_tiles() -> Sequence[tuple]:
     """Instantiated (kind, rows_per_group, cols_per_wave, waves_per_group, depth) tuples."""
     out = []
-    for kind in (1, 2, 3):
+    for kind in (1, 2, 3, 4):
         for rows in ((1, 2, 4, 8) if kind == 3 else (16, 32, 64)):
             for cols in (16, 32, 64, 128):
                 for waves in (1, 2, 4, 8):
@@ -522,8 +521,8 @@ def kernel_tiles() -> Sequence[tuple]:
 
 def __getattr__(name: str):
     if name == "_PREPACK_AUTOTUNE_CONFIGS":
-        cfgs = [TileConfig({"BLOCK_B": r, "BLOCK_N": c * (w if k == 2 else 1)}, num_warps=w, num_stages=d, kind=k)
-                for (k, r, c, w, d) in kernel_tiles()]
+        cfgs = [TileConfig({"BLOCK_B": r, "BLOCK_N": Plan(1, c, w, d, r, k).group_cols()}, num_warps=w,
+                           num_stages=d, kind=k) for (k, r, c, w, d) in kernel_tiles()]
         globals()[name] = cfgs
         return cfgs
     raise AttributeError(name)

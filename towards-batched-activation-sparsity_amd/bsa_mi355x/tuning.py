@@ -253,8 +253,7 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
                 entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": na, "dense": False,
                                 "plan": list(best[1].as_tuple()), "us": round(best[0], 3)})
                 t = best[1]
-                tile = [t.rows_per_group, t.cols_per_wave * (t.waves_per_group if t.kind == 2 else 1),
-                        t.waves_per_group, t.depth]
+                tile = [t.rows_per_group, t.group_cols(), t.waves_per_group, t.depth]
                 rec = {"mask": "naive", "block_k": BLOCK_K, "K": t.split_k, "tile": tile,
                        "best_kern": "naive", "best_K": t.split_k, "best_tile": tile,
                        "dense_ms": dense_best[0] / 1000.0, "sparse_ms": best[0] / 1000.0,

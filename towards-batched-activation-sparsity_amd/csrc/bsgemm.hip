@@ -460,24 +460,32 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
 }
 
-// Kind 2 ("xlds"): one work-group = BTT*16 batch rows x WPG*NSUB*16 columns; its waves split
-// the columns and walk the same block list together.  Each block's X tile (BTT*16 rows x 64
-// channels) is loaded once per work-group, in MFMA B-fragment order, into a double-buffered
-// LDS stage (one barrier per block) and shared by every wave, so X costs 1/WPG of the loads
-// of kind 1 and the prefetch registers hold weights only.  Best for larger batches.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
-__global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
+// Kinds 2 and 4 ("xlds"): one work-group = BTT*16 batch rows x WC*NSUB*16 columns; its waves
+// walk the same block list together.  Each block's X tile (BTT*16 rows x 64 channels) is loaded
+// once per work-group, in MFMA B-fragment order, into a double-buffered LDS stage (one barrier
+// per block) and shared by every wave, so X costs 1/WPG of the loads of kind 1 and the prefetch
+// registers hold weights only.  Kind 2 (WK = 1): the WC waves split the columns.  Kind 4
+// (WK = 2): 2*WC waves, column group x 32-channel half of every block, so each wave issues half
+// the MFMAs and LDS reads of a block and two waves share each SIMD, overlapping one wave's
+// barrier and LDS waits with the other's MFMAs; the halves are summed through LDS at the end.
+template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH>
+__global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p) {
+  constexpr int WPG = WC * WK;
   constexpr int NT = 64 * WPG;
   constexpr int XF = 2 * BTT;                // X fragments (1 KiB each) per block
   constexpr int XPW = (XF + WPG - 1) / WPG;  // X fragments each wave loads per block
-  constexpr int CS = WPG * NSUB;             // 16-column subtiles per work-group
+  constexpr int CS = WC * NSUB;              // 16-column subtiles per work-group
   constexpr int FT = BTT * CS;               // output fragments per work-group
+  constexpr int HPW = 2 / WK;                // channel halves per wave
   __shared__ int s_ids[BSG_MAX_NBLK];
   __shared__ __attribute__((aligned(16))) u32x4 s_x[2][XF][64];
+  __shared__ __attribute__((aligned(16))) f32x4 s_red[WK > 1 ? WC * BTT * NSUB : 1][64];
   __shared__ int s_misc[WPG + 2];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wc = w % WC;  // column group
+  const int wk = w / WC;  // channel half (kind 4)
   int tile, sk;
   tile_of_group(p.split_k, &tile, &sk);
   const int S = p.split_k;
@@ -505,9 +513,9 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
     xrow_off[j] = xrow_ok[j] ? row * (int)p.ldx * 2 : 0;
     xcol[j] = 32 * (f & 1) + 8 * (lane >> 4);
   }
-  const int wcol = lane * 16 + ((n0 >> 4) + w * NSUB) * 2048;
+  const int wcol = lane * 16 + ((n0 >> 4) + wc * NSUB) * 2048;
 
-  u32x4 wv[DEPTH][NSUB][2];
+  u32x4 wv[DEPTH][NSUB][HPW];
   u32x4 xs[DEPTH][XPW];
   f32x4 acc[BTT][NSUB];
 #pragma unroll
@@ -515,7 +523,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto issue = [&](u32x4 (&wd)[NSUB][2], u32x4 (&xd)[XPW], int t) {
+  auto issue = [&](u32x4 (&wd)[NSUB][HPW], u32x4 (&xd)[XPW], int t) {
     const int q = t < cnt ? pbeg + t : 0;
     int blk = s_ids[q];
     blk = __builtin_amdgcn_readfirstlane(blk);
@@ -523,10 +531,9 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
-      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
-    }
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) wd[s][hh] = ld16_stream(wr, wcol + s * 2048 + (WK > 1 ? wk : hh) * 1024);
     const int kb = (ok ? blk : 0) * 64;
 #pragma unroll
     for (int j = 0; j < XPW; ++j) {
@@ -549,29 +556,49 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_xl_kernel(GemmParams p) {
         if (w + j * WPG < XF) s_x[stage][w + j * WPG][lane] = xs[d][j];
       __syncthreads();
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int hh = 0; hh < HPW; ++hh) {
+        const int h = WK > 1 ? wk : hh;
 #pragma unroll
         for (int bi = 0; bi < BTT; ++bi) {
           const u32x4 xb = s_x[stage][2 * bi + h][lane];
 #pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][h], xb, acc[bi][s]);
+          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xb, acc[bi][s]);
         }
       }
       issue(wv[d], xs[d], t0 + d + DEPTH);
     }
   }
 
-  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
+  if constexpr (WK > 1) {
+    // The second channel half hands its accumulators to the first through LDS.
+    if (wk == 1) {
 #pragma unroll
-  for (int bi = 0; bi < BTT; ++bi)
+      for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      const int g = bi * CS + w * NSUB + s;
-      if (S == 1)
-        store_y<T, CS>(p, y0, n0, g, acc[bi][s]);
-      else
-        part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
+        for (int s = 0; s < NSUB; ++s) s_red[(wc * BTT + bi) * NSUB + s][lane] = acc[bi][s];
     }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] += s_red[(wc * BTT + bi) * NSUB + s][lane];
+    }
+  }
+
+  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
+  if (wk == 0) {
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) {
+        const int g = bi * CS + wc * NSUB + s;
+        if (S == 1)
+          store_y<T, CS>(p, y0, n0, g, acc[bi][s]);
+        else
+          part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
+      }
+  }
   if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
 }
 
@@ -1087,7 +1114,7 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
 
 typedef void (*GemmFn)(GemmParams);
 
-enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3 };
+enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4 };
 
 struct KernelEntry {
   int kind, rows, nsub, wpg, depth;
@@ -1097,7 +1124,10 @@ struct KernelEntry {
 #define BSG_K(B, S, W, D) \
   {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
 #define BSG_X(B, S, W, D) \
-  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, D>}
+  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D>}
+#define BSG_Y(B, S, W, D)                                                             \
+  {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D>, \
+   bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D>}
 #define BSG_F(R, S, W, D) \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D>, bsg_gemm_fma_kernel<__bf16, R, S, W, D>}
 
@@ -1128,6 +1158,11 @@ const KernelEntry kKernels[] = {
     BSG_X(2, 1, 2, 4), BSG_X(2, 1, 4, 4), BSG_X(2, 1, 4, 8), BSG_X(2, 2, 2, 4), BSG_X(2, 2, 4, 4),
     BSG_X(4, 1, 2, 4), BSG_X(4, 1, 4, 4), BSG_X(4, 1, 4, 8), BSG_X(4, 1, 8, 4), BSG_X(4, 2, 2, 2),
     BSG_X(4, 2, 2, 4), BSG_X(4, 2, 4, 2), BSG_X(4, 2, 4, 4), BSG_X(4, 4, 2, 2), BSG_X(4, 4, 4, 2),
+    // kind 4 (as kind 2, waves also split the two channel halves of every block)
+    BSG_Y(4, 1, 8, 4), BSG_Y(4, 1, 8, 2), BSG_Y(4, 1, 8, 8), BSG_Y(4, 2, 8, 2), BSG_Y(4, 2, 8, 4),
+    BSG_Y(4, 1, 4, 4), BSG_Y(4, 2, 4, 4), BSG_Y(4, 1, 4, 8),
+    BSG_Y(2, 1, 8, 4), BSG_Y(2, 1, 4, 4), BSG_Y(2, 2, 4, 4),
+    BSG_Y(1, 1, 8, 4), BSG_Y(1, 1, 4, 4),
     // kind 3 (fp32 dot products, 1-8 batch rows, X staged in LDS)
     BSG_F(1, 1, 2, 4), BSG_F(1, 1, 4, 4), BSG_F(1, 1, 4, 8), BSG_F(1, 1, 8, 4), BSG_F(1, 2, 4, 4),
     BSG_F(2, 1, 2, 4), BSG_F(2, 1, 4, 4), BSG_F(2, 1, 4, 8), BSG_F(2, 1, 8, 4), BSG_F(2, 2, 4, 4),
@@ -1137,6 +1172,7 @@ const KernelEntry kKernels[] = {
 #undef BSG_K
 #undef BSG_X
 #undef BSG_F
+#undef BSG_Y
 
 const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
   for (const KernelEntry& e : kKernels)
@@ -1162,7 +1198,9 @@ bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1))
 
 // Columns covered by one work-group of a resolved plan.
 int64_t group_cols(const bsg_plan* pl) {
-  return (int64_t)pl->cols_per_wave * (pl->kind == KIND_XLDS ? pl->waves_per_group : 1);
+  if (pl->kind == KIND_XLDS) return (int64_t)pl->cols_per_wave * pl->waves_per_group;
+  if (pl->kind == KIND_XLDS_KH) return (int64_t)pl->cols_per_wave * (pl->waves_per_group / 2);
+  return pl->cols_per_wave;
 }
 
 int resolve_fma(int64_t bt, int32_t na, bsg_plan* pl) {
@@ -1191,9 +1229,9 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
   if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
     return fail(BSG_ERR_ARG, "plan: bt=%lld N=%lld nblk=%d na=%d cu=%d", (long long)bt, (long long)N,
                 nblk, na, cu);
-  if (pl->kind < 0 || pl->kind > KIND_FMA)
+  if (pl->kind < 0 || pl->kind > KIND_XLDS_KH)
     return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X tile in LDS, "
-                "3 = fp32 dot products for 1-8 rows)", pl->kind);
+                "3 = fp32 dot products for 1-8 rows, 4 = as 2 with channel-half waves)", pl->kind);
   // The dot-product kernel (kind 3) runs when a plan names it; automatic plans use the MFMA
   // kinds, which measure faster at every batch size on gfx950.
   if (pl->rows_per_group == 0 && pl->kind == KIND_FMA) pl->rows_per_group = bt <= 8 ? pow2_ceil(bt) : 8;
@@ -1211,7 +1249,7 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
     if (pl->depth == 0) pl->depth = rpg == 64 ? 2 : 4;
   } else {
     if (pl->cols_per_wave == 0) pl->cols_per_wave = 16;
-    if (pl->waves_per_group == 0) pl->waves_per_group = 4;
+    if (pl->waves_per_group == 0) pl->waves_per_group = pl->kind == KIND_XLDS_KH ? 8 : 4;
     if (pl->depth == 0) pl->depth = 4;
   }
   if (!pow2_in(pl->cols_per_wave, 16, 128) || !pow2_in(pl->waves_per_group, 1, 8) ||
