@@ -2,6 +2,7 @@
 reference tile -> plan mapping, and the drop-in module path."""
 from __future__ import annotations
 
+import ctypes
 import json
 import os
 
@@ -18,8 +19,14 @@ def test_shipped_table_covers_baseline_shapes():
     assert {(4096, 4096), (11008, 4096), (4096, 11008)} <= shapes
     assert {e["bt"] for e in entries} >= {2, 16, 64}
     assert any(e["dense"] for e in entries)
+    lib = bsa.load()
     for e in entries:
-        assert len(e["plan"]) == 6 and e["plan"][0] >= 1 and e["plan"][5] in (1, 2)
+        assert len(e["plan"]) == 6 and e["plan"][0] >= 1 and e["plan"][5] in (1, 2, 3, 4)
+        # every shipped plan names an instantiated kernel the library accepts as is
+        p = bsa.Plan(*e["plan"])
+        want = p.as_tuple()
+        assert lib.bsg_plan_resolve(e["bt"], e["N"], -(-e["K"] // 64), e["na"], 256, ctypes.byref(p)) == 0, e
+        assert p.as_tuple() == want, (e, p.as_tuple())
 
 
 def test_lookup_nearest_batch_and_density():
