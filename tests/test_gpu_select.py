@@ -6,6 +6,7 @@ import pytest
 import torch
 
 import bsa_mi355x as bsa
+from bsa_mi355x.select import select_gemm_packed
 from helpers import assert_close, case, to_dev
 from oracle import bsg_oracle as orc
 
@@ -73,6 +74,59 @@ def test_fused_select_gemm(dev, shape, bt, k):
     assert np.array_equal(idx.cpu().numpy(), want)
     assert int(cnt.item()) == k
     assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), "fused select+gemm")
+
+
+def _fused(dev, x, w_nk, k, plan=None):
+    bt, kdim = x.shape
+    n = w_nk.shape[0]
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    y = torch.empty(bt, n, dtype=torch.float16, device=dev)
+    idx, cnt = select_gemm_packed(to_dev(x, dev), packed, n, k, y,
+                                  plan=None if plan is None else bsa.Plan(*plan), workspace_prefix="t_fused")
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    return idx.cpu().numpy()[:c], c, y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("bt,kdim,n,k,plan", [
+    (64, 4096, 11008, 31, (1, 16, 8, 4, 64, 4)),  # channel-half waves; ranked in the GEMM
+    (64, 4096, 4096, 31, (2, 16, 4, 4, 64, 2)),   # X tile in LDS, split-K 2; in the GEMM
+    (64, 11008, 4096, 83, (4, 16, 8, 4, 64, 4)),  # 172 blocks over 8 waves; in the GEMM
+    (16, 4096, 4096, 23, (1, 16, 1, 4, 16, 1)),   # one wave ranks 64 blocks; in the GEMM
+    (16, 11008, 4096, 86, (1, 16, 2, 4, 16, 1)),  # 172 blocks, 2 waves: rank launch, then the list
+    (2, 4096, 4096, 13, (1, 16, 4, 4, 2, 3)),     # dot-product kernel; in the GEMM
+    (80, 4096, 1024, 20, None),                   # > 64 rows: pair compares, two grid rows
+    (8, 32768, 256, 100, (1, 16, 1, 4, 16, 1)),   # 512 blocks: rank launch
+    (4, 38400, 256, 77, None),                    # 600 blocks: rank launch
+    (16, 4096, 512, 0, None), (16, 4096, 512, 64, None), (16, 4096, 512, 200, None),
+])
+def test_fused_select_gemm_every_kind(dev, bt, kdim, n, k, plan):
+    """Selection + GEMM for every kernel kind and edge k, with the top-k either ranked inside
+    the GEMM's work-groups or by a separate rank launch (the library picks by plan); the kept
+    list and count are published either way."""
+    x, w_nk, _ = case(4321 + bt + k, bt, kdim, n, 1, "normal")
+    got, c, y = _fused(dev, x, w_nk, k, plan)
+    want = orc.select_topk_l1(x, k)
+    assert c == len(want) == min(k, -(-kdim // 64))
+    assert np.array_equal(got, want)
+    assert_close(y, orc.gemm_ref(x, w_nk, want), f"fused bt={bt} K={kdim} k={k} plan={plan}")
+
+
+def test_fused_select_gemm_ties_and_repeats(dev):
+    """Equal scores go to the lower index inside the GEMM's own ranking, and a second call on
+    new activations (same workspace) selects afresh."""
+    bt, kdim, n = 8, 4096, 256
+    x, w_nk, _ = case(77, bt, kdim, n, 1, "normal")
+    for j in (10, 20, 30):
+        x[:, 64 * j:64 * j + 64] = 50.0
+    got, c, y = _fused(dev, x, w_nk, 2)
+    assert c == 2 and np.array_equal(got, [10, 20])
+    assert_close(y, orc.gemm_ref(x, w_nk, [10, 20]), "fused ties")
+    x2, _, _ = case(78, bt, kdim, n, 1, "normal")
+    got2, c2, y2 = _fused(dev, x2, w_nk, 9)
+    want2 = orc.select_topk_l1(x2, 9)
+    assert c2 == 9 and np.array_equal(got2, want2)
+    assert_close(y2, orc.gemm_ref(x2, w_nk, want2), "fused repeat")
 
 
 def test_select_density_wrapper(dev):

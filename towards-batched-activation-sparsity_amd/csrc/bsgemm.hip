@@ -61,7 +61,10 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kOOB = (int)0x80000000u;  // buffer offset beyond any num_records we build
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 
-enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2 };
+enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2, MODE_TOPK = 3 };
+// A GEMM ranks block scores itself (MODE_TOPK) up to this many blocks: keys and ranks fit its
+// block-list buffer, and a one-wave work-group flags at most 8 per thread.
+#define BSG_TOPK_MAX_NBLK 512
 
 // Kind 3 activation staging: 1 KiB loads per wave, and the LDS it may take.
 #define BSG_FMA_X_LOADS 16
@@ -141,6 +144,125 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* scratch, int* total
   return base + incl - v;
 }
 
+// The one-work-group top-k (1024 threads) flags at most 2 blocks per thread (kept flags: one
+// 32-bit mask per thread).
+static_assert(BSG_MAX_NBLK <= 32 * 1024, "selector chunk layout");
+
+// Rank of block j among nb scores in LDS, ordered (score desc, block id asc): the number of
+// blocks ahead of it.  s_sc holds the nb scores followed by zeros up to a multiple of 16 (a pad
+// is never ahead: its score is the lowest and its id >= nb).  The scores are read as LDS
+// broadcasts into two 8-score buffers, each refilled while the other is compared, so the loop
+// runs at the compare rate rather than the LDS round trip.  UNIQUE: the scores are distinct keys
+// that already encode the id order, so one compare does.  Rolled on purpose: a work-group runs
+// it once, so unrolled copies cost more in cold instruction fetch than they save.
+template <bool UNIQUE, typename S>
+__device__ __forceinline__ int rank_of(const S* s_sc, int nb, int j, S sj) {
+  const int nb16 = (nb + 15) & ~15;
+  int rank = 0;
+  S a[8], b[8];
+  auto count = [&](const S (&v)[8], int i0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if constexpr (UNIQUE)
+        rank += v[u] > sj;
+      else
+        rank += (v[u] > sj) | ((v[u] == sj) & (i0 + u < j));
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = s_sc[u];
+#pragma unroll 1
+  for (int i0 = 0; i0 < nb16; i0 += 16) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b[u] = s_sc[i0 + 8 + u];
+    __builtin_amdgcn_sched_barrier(0);
+    count(a, i0);
+    const int in = i0 + 16 < nb16 ? i0 + 16 : 0;  // the last refill is a harmless re-read
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = s_sc[in + u];
+    __builtin_amdgcn_sched_barrier(0);
+    count(b, i0 + 8);
+  }
+  return rank;
+}
+
+// Zero the pad of a score array after its nb entries, up to a multiple of 16 (rank_of).
+template <typename S>
+__device__ __forceinline__ void pad_scores(S* s_sc, int nb) {
+  const int tid = threadIdx.x;
+  if (tid < ((nb + 15) & ~15) - nb) s_sc[nb + tid] = S(0);
+}
+
+// Top-k of nb exact-L1 block scores (global memory, written by an earlier kernel on the
+// stream): ranked (score desc, id asc), the first k kept, their ids handed to emit(position,
+// id) in ascending id order.  keyed: every score is below 2^53, so (score << 11) | (2047 - id)
+// is a unique key in the same order and one compare decides.  The nb^2 compares are spread over
+// every wave of the work-group: a work item is (64 blocks, 16 scores), each lane counts the
+// scores ahead of its block and adds the count to the block's rank in LDS.  s_key holds nb
+// keys rounded up to 16, s_rank nb ints; each thread then flags a contiguous chunk of at most
+// 32 blocks (nb <= 32 * NT), so a scan of the counts gives ascending positions.  Returns
+// min(k, nb).  Every thread has finished reading s_key and s_rank when emit runs (the scan's
+// barriers lie between), so emit may overwrite them.
+template <int NT, typename Emit>
+__device__ __forceinline__ int topk_l1_list(const uint64_t* scores, int nb, int k, bool keyed, uint64_t* s_key,
+                                            int* s_rank, int* s_scan, Emit emit) {
+  constexpr int W = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb16 = (nb + 15) & ~15;
+  for (int i = tid; i < nb16; i += NT) {
+    uint64_t key = 0;  // pads: lowest score, ids >= nb, never ahead
+    if (i < nb) {
+      const uint64_t v = scores[i];
+      key = keyed ? (v << 11) | (uint64_t)(BSG_MAX_NBLK - 1 - i) : v;
+    }
+    s_key[i] = key;
+  }
+  for (int i = tid; i < nb; i += NT) s_rank[i] = 0;
+  __syncthreads();
+  const int C = nb16 / 16;
+  const int items = ((nb + 63) / 64) * C;
+#pragma unroll 1
+  for (int it = w; it < items; it += W) {
+    const int g = it / C;
+    const int i0 = 16 * (it - g * C);
+    const int j = 64 * g + lane;
+    const uint64_t kj = j < nb ? s_key[j] : 0;
+    uint64_t ki[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) ki[u] = s_key[i0 + u];
+    int r = 0;
+    if (keyed) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) r += ki[u] > kj;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) r += (ki[u] > kj) | ((ki[u] == kj) & (i0 + u < j));
+    }
+    if (j < nb && r != 0) atomicAdd(&s_rank[j], r);
+  }
+  __syncthreads();
+  const int per = (nb + NT - 1) / NT;
+  const int beg = tid * per < nb ? tid * per : nb;
+  const int end = beg + per < nb ? beg + per : nb;
+  const int kk = k < nb ? k : nb;
+  uint32_t selmask = 0;
+  int c = 0;
+#pragma unroll 1
+  for (int q = 0; q < end - beg; ++q)
+    if (s_rank[beg + q] < kk) {
+      selmask |= 1u << q;
+      ++c;
+    }
+  int total = 0;
+  int o = wg_exclusive_scan<NT>(c, s_scan, &total);
+#pragma unroll 1
+  for (int q = 0; q < end - beg; ++q)
+    if ((selmask >> q) & 1u) emit(o++, beg + q);
+  return kk;
+}
+
+
 // Split-K hand-off primitives.  Partials move with agent-scope relaxed atomics, which are
 // device-coherent without touching the rest of L2 (an agent-scope fence would write back and
 // invalidate the whole L2 of the XCD on every work-group).
@@ -184,6 +306,12 @@ struct GemmParams {
   int64_t ldx;
   int64_t ldy;
   int32_t bt, K, N, npad, nblk, nbm, na, mode, split_k, n_tiles, x_bytes, y_fast;
+  // MODE_TOPK: exact-L1 block scores (na = k), whether they fit the unique-key order, and where
+  // work-group (0, 0) publishes the kept list and its count (null: not published)
+  const uint64_t* scores;
+  int32_t* idx_out;
+  int32_t* na_out;
+  int32_t keyed;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -199,13 +327,20 @@ __device__ __forceinline__ void tile_of_group(int split_k, int* tile, int* sk) {
   *sk = lid - *tile * split_k;
 }
 
-// Stage this call's active-block list in LDS (list copy, bitmap compaction or identity) and
-// return its length.  Ends with a barrier.
+// Stage this call's active-block list in LDS (list copy, bitmap compaction, top-k of block
+// scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
+// and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
+// second (up to 512 blocks).
 template <int NT>
 __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
   const int tid = threadIdx.x;
   int na;
-  if (p.mode == MODE_LIST) {
+  if (p.mode == MODE_TOPK) {
+    // Every work-group ranks the scores itself (identically), so the list needs no other
+    // launch; keys and ranks are staged in the list buffer and overwritten by the kept ids.
+    na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
+                          s_scan, [&](int pos, int id) { s_ids[pos] = id; });
+  } else if (p.mode == MODE_LIST) {
     na = p.na;
     if (p.na_dev != nullptr) {
       const int d = *p.na_dev;
@@ -229,6 +364,10 @@ __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids,
   }
   na = __builtin_amdgcn_readfirstlane(na);
   __syncthreads();
+  if (p.mode == MODE_TOPK && p.idx_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+    for (int i = tid; i < na; i += NT) p.idx_out[i] = s_ids[i];
+    if (tid == 0) *p.na_out = na;
+  }
   return na;
 }
 
@@ -477,7 +616,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   constexpr int CS = WC * NSUB;              // 16-column subtiles per work-group
   constexpr int FT = BTT * CS;               // output fragments per work-group
   constexpr int HPW = 2 / WK;                // channel halves per wave
-  __shared__ int s_ids[BSG_MAX_NBLK];
+  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
   __shared__ __attribute__((aligned(16))) u32x4 s_x[2][XF][64];
   __shared__ __attribute__((aligned(16))) f32x4 s_red[WK > 1 ? WC * BTT * NSUB : 1][64];
   __shared__ int s_misc[WPG + 2];
@@ -615,7 +754,7 @@ template <typename T, int BT, int NSUB, int WPG, int DEPTH>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
   constexpr int XI = BSG_FMA_X_LOADS;  // staging loads per wave (host guarantees enough)
-  __shared__ int s_ids[BSG_MAX_NBLK];
+  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
   __shared__ float s_red[WPG > 1 ? WPG - 1 : 1][NSUB * BT][16];
   __shared__ int s_misc[WPG + 2];
   extern __shared__ __attribute__((aligned(16))) u32x4 s_xs[];  // [na][BT][2][4]
@@ -778,7 +917,6 @@ struct SelScoreParams {
   const float* scale;
   double* scores;
   double* energy;
-  uint32_t* cnt;
   int32_t* idx_out;
   int32_t* na_out;
   float* ratio_out;
@@ -798,16 +936,8 @@ __device__ __forceinline__ float elem_to_float<__bf16>(uint32_t b) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void bsg_select_score_kernel(SelScoreParams p) {
-  __shared__ double s_sc[BSG_MAX_NBLK];
-  __shared__ double s_en[BSG_MAX_NBLK];
-  __shared__ int s_order[BSG_MAX_NBLK];
-  __shared__ uint8_t s_sel[BSG_MAX_NBLK];
+__global__ __launch_bounds__(256) void bsg_score_rule_kernel(SelScoreParams p) {
   __shared__ double s_part[3][4];
-  __shared__ double s_csum[256];
-  __shared__ double s_total;
-  __shared__ int s_scan[4];
-  __shared__ int s_last, s_keep, s_first;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = blockIdx.x;
 
@@ -864,33 +994,32 @@ __global__ __launch_bounds__(256) void bsg_select_score_kernel(SelScoreParams p)
       const double pr = (double)p.prior[j] + (double)p.eps;
       sc *= pow(pr > 1e-6 ? pr : 1e-6, (double)p.alpha);
     }
-    // Score and energy out through agent-scope stores; once they have completed, count the
-    // arrival (the last work-group reads them with agent-scope loads).
-    __hip_atomic_store(&p.scores[j], sc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&p.energy[j], en, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    const unsigned prev = __hip_atomic_fetch_add(p.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(p.nb - 1);
+    p.scores[j] = sc;
+    p.energy[j] = en;
   }
-  __syncthreads();
-  if (!s_last) return;
+}
 
+// One work-group after bsg_score_rule_kernel on the same stream (the launch boundary orders
+// the scores before these loads): ranks, applies the energy budget, writes the kept ids.
+__global__ __launch_bounds__(256) void bsg_rank_rule_kernel(SelScoreParams p) {
+  __shared__ double s_sc[BSG_MAX_NBLK];
+  __shared__ double s_en[BSG_MAX_NBLK];
+  __shared__ int s_order[BSG_MAX_NBLK];
+  __shared__ uint8_t s_sel[BSG_MAX_NBLK];
+  __shared__ double s_csum[256];
+  __shared__ double s_total;
+  __shared__ int s_scan[4];
+  __shared__ int s_keep, s_first;
+  const int tid = threadIdx.x;
   const int nb = p.nb;
   for (int i = tid; i < nb; i += 256) {
-    s_sc[i] = __hip_atomic_load(&p.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_en[i] = __hip_atomic_load(&p.energy[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_sc[i] = p.scores[i];
+    s_en[i] = p.energy[i];
   }
+  pad_scores(s_sc, nb);
   __syncthreads();
   // rank of every block; order[rank] = block
-  for (int jj = tid; jj < nb; jj += 256) {
-    const double sj = s_sc[jj];
-    int rank = 0;
-    for (int i = 0; i < nb; ++i) {
-      const double si = s_sc[i];
-      rank += (si > sj) || (si == sj && i < jj);
-    }
-    s_order[rank] = jj;
-  }
+  for (int j = tid; j < nb; j += 256) s_order[rank_of<false>(s_sc, nb, j, s_sc[j])] = j;
   const int k0 = p.k < nb ? p.k : nb;
   if (tid == 0) {
     s_keep = k0;
@@ -952,10 +1081,7 @@ __global__ __launch_bounds__(256) void bsg_select_score_kernel(SelScoreParams p)
   int o = wg_exclusive_scan<256>(c, s_scan, &total);
   for (int jj = beg; jj < end; ++jj)
     if (s_sel[jj]) p.idx_out[o++] = jj;
-  if (tid == 0) {
-    *p.na_out = keep;
-    __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid == 0) *p.na_out = keep;
 }
 // Read-rate calibration (no counterpart in the reference): streams `bytes` from src with the
 // access pattern of the GEMM's weight stream (one 1 KiB wave-load per 16-byte lane slice,
@@ -1031,19 +1157,17 @@ struct SelParams {
   const uint16_t* x;
   int64_t ldx;
   uint64_t* scores;
-  uint32_t* cnt;
   int32_t* idx_out;
   int32_t* na_out;
   int32_t bt, K, nblk, k;
 };
 
-// Fused selector: work-group j scores block j; the last work-group to finish ranks all
-// blocks by (score desc, id asc), keeps the first k and writes them in ascending id order.
-__global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
-  __shared__ uint64_t s_sc[BSG_MAX_NBLK];
+// Exact-L1 selector, first launch: work-group j sums |x| over block j and every row, in exact
+// integer units, and stores it.  The ranking (bsg_rank_l1_kernel, or a GEMM in top-k mode) is a
+// separate launch: a last-arriver hand-off would put every work-group's increment on one
+// device-scope counter, and those serialize (4-7 us at 64-172 blocks, measured).
+__global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
   __shared__ uint64_t s_part[4];
-  __shared__ int s_scan[4];
-  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = blockIdx.x;
 
@@ -1063,50 +1187,18 @@ __global__ __launch_bounds__(256) void bsg_select_l1_kernel(SelParams p) {
   for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
   if (lane == 0) s_part[w] = acc;
   __syncthreads();
-  if (tid == 0) {
-    // Score out through an agent-scope (device-coherent) store; once it has completed, count
-    // the arrival.  The last work-group reads every score with agent-scope loads.  No L2
-    // write-back/invalidate is involved.
-    __hip_atomic_store(&p.scores[j], s_part[0] + s_part[1] + s_part[2] + s_part[3], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    const unsigned prev = __hip_atomic_fetch_add(p.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(p.nblk - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
+  if (tid == 0) p.scores[j] = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+}
 
-  const int nb = p.nblk;
-  for (int i = tid; i < nb; i += 256)
-    s_sc[i] = __hip_atomic_load(&p.scores[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const int per = (nb + 255) / 256;
-  const int beg = tid * per < nb ? tid * per : nb;
-  const int end = beg + per < nb ? beg + per : nb;
-  const int k = p.k < nb ? p.k : nb;
-  // selected flags of this thread's chunk, packed into a 64-bit mask (per <= 8 here)
-  uint64_t selmask = 0;
-  int c = 0;
-  for (int jj = beg; jj < end; ++jj) {
-    const uint64_t sj = s_sc[jj];
-    int rank = 0;
-    for (int i = 0; i < nb; ++i) {
-      const uint64_t si = s_sc[i];
-      rank += (si > sj) || (si == sj && i < jj);
-    }
-    if (rank < k) {
-      selmask |= 1ull << (jj - beg);
-      ++c;
-    }
-  }
-  int total = 0;
-  int o = wg_exclusive_scan<256>(c, s_scan, &total);
-  for (int jj = beg; jj < end; ++jj)
-    if (selmask & (1ull << (jj - beg))) p.idx_out[o++] = jj;
-  if (tid == 0) {
-    *p.na_out = k;
-    __hip_atomic_store(p.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+// One work-group after bsg_score_l1_kernel on the same stream (the launch boundary orders the
+// scores before these loads): the top-k, written ascending with its count.
+__global__ __launch_bounds__(1024) void bsg_rank_l1_kernel(SelParams p) {
+  __shared__ __attribute__((aligned(16))) uint64_t s_key[BSG_MAX_NBLK];
+  __shared__ int s_rank[BSG_MAX_NBLK];
+  __shared__ int s_scan[16];
+  const int k = topk_l1_list<1024>(p.scores, p.nblk, p.k, p.bt <= 64, s_key, s_rank, s_scan,
+                                  [&](int pos, int id) { p.idx_out[pos] = id; });
+  if (threadIdx.x == 0) *p.na_out = k;
 }
 
 // ----------------------------------------------------------------------------------------
@@ -1348,16 +1440,24 @@ int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* 
   return BSG_OK;
 }
 
+// MODE_TOPK: na is k, scores the exact-L1 block scores; the kept list and its count are
+// published to idx_out / na_out (when not null) by work-group (0, 0).
 int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp,
                 int64_t N, const int32_t* idx, int32_t na, const int32_t* na_dev,
                 const uint8_t* bitmap, int32_t nbm, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
-                const bsg_plan* plan_in, void* stream) {
+                const bsg_plan* plan_in, void* stream, const uint64_t* scores = nullptr,
+                int32_t* idx_out = nullptr, int32_t* na_out = nullptr) {
   int rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype);
   if (rc != BSG_OK || bt == 0) return rc;
   const int32_t nblk = (int32_t)cdiv(K, BSG_BLOCK_K);
   if (mode == MODE_LIST) {
     if (na < 0 || na > BSG_MAX_NBLK) return fail(BSG_ERR_ARG, "num_active=%d (0..%d)", na, BSG_MAX_NBLK);
     if (na > 0 && !idx) return fail(BSG_ERR_ARG, "active_blocks is null");
+  } else if (mode == MODE_TOPK) {
+    if (!scores || na < 0) return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)scores, na);
+    if (nblk > BSG_TOPK_MAX_NBLK)
+      return fail(BSG_ERR_UNSUPPORTED, "top-k in the GEMM: %d blocks (at most %d)", nblk, BSG_TOPK_MAX_NBLK);
+    if (na > nblk) na = nblk;
   } else if (mode == MODE_BITMAP) {
     if (!bitmap) return fail(BSG_ERR_ARG, "bitmap is null");
     if (nbm < 1 || nbm > nblk)
@@ -1408,6 +1508,10 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.n_tiles = (int32_t)n_tiles;
   p.x_bytes = (int32_t)(((bt - 1) * ldx + K) * 2);
   p.y_fast = (N % 4 == 0) && (ldy % 4 == 0) && (((uintptr_t)y & 7u) == 0);
+  p.scores = scores;
+  p.idx_out = idx_out;
+  p.na_out = na_out;
+  p.keyed = bt <= 64;
 
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
@@ -1504,8 +1608,9 @@ int64_t bsg_select_workspace_bytes(int64_t K) {
   return cdiv(256 + cdiv(K, BSG_BLOCK_K) * 16, 256) * 256;
 }
 
-int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
-                       int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
+// Checks, then the score launch and (rank) the top-k launch of the exact-L1 selector.
+static int select_l1_launch(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
+                            int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream, bool rank) {
   if (dtype != BSG_F16)
     return fail(BSG_ERR_DTYPE, "select: exact L1 scoring is defined for fp16 inputs (dtype=%d)", dtype);
   if (bt <= 0 || K <= 0) return fail(BSG_ERR_ARG, "select: bt=%lld K=%lld", (long long)bt, (long long)K);
@@ -1523,7 +1628,6 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
   SelParams p;
   p.x = (const uint16_t*)x;
   p.ldx = ldx;
-  p.cnt = (uint32_t*)ws;
   p.scores = (uint64_t*)((char*)ws + 256);
   p.idx_out = idx_out;
   p.na_out = na_out;
@@ -1531,10 +1635,19 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
   p.K = (int32_t)K;
   p.nblk = (int32_t)nblk;
   p.k = k;
-  hipLaunchKernelGGL(bsg_select_l1_kernel, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(bsg_score_l1_kernel, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 launch");
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 score launch");
+  if (!rank) return BSG_OK;
+  hipLaunchKernelGGL(bsg_rank_l1_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 rank launch");
   return BSG_OK;
+}
+
+int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
+                       int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
+  return select_l1_launch(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream, true);
 }
 
 int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
@@ -1571,7 +1684,6 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
   p.ldx = ldx;
   p.prior = o.block_prior;
   p.scale = o.channel_scale;
-  p.cnt = (uint32_t*)ws;
   p.scores = (double*)((char*)ws + 256);
   p.energy = p.scores + cdiv(K, BSG_BLOCK_K);
   p.idx_out = idx_out;
@@ -1586,11 +1698,14 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
   p.k = k;
   p.mode = o.score;
   if (dtype == BSG_F16)
-    hipLaunchKernelGGL(bsg_select_score_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(bsg_score_rule_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL(bsg_select_score_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(bsg_score_rule_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk launch");
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk score launch");
+  hipLaunchKernelGGL(bsg_rank_rule_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk rank launch");
   return BSG_OK;
 }
 
@@ -1615,12 +1730,31 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
                     const bsg_plan* plan, void* stream) {
   const int64_t sel = bsg_select_workspace_bytes(K);
   if (sel < 0) return fail(BSG_ERR_ARG, "select_gemm: K=%lld", (long long)K);
-  int rc = bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
-  if (rc != BSG_OK) return rc;
   const int64_t nblk = cdiv(K, BSG_BLOCK_K);
+  if (k < 0) return fail(BSG_ERR_ARG, "select_gemm: k=%d", k);
+  if (bt <= 0 || N <= 0 || nblk > BSG_MAX_NBLK)
+    return fail(BSG_ERR_ARG, "select_gemm: bt=%lld N=%lld K=%lld", (long long)bt, (long long)N, (long long)K);
+  bsg_plan pl = plan ? *plan : bsg_plan{0, 0, 0, 0, 0, 0};
   const int32_t kk = k < nblk ? k : (int32_t)nblk;
+  int rc = resolve(bt, N, (int32_t)nblk, kk, pl.split_k == 0 ? device_cu_count() : 256, &pl);
+  if (rc != BSG_OK) return rc;
+  // The GEMM ranks the scores itself when every work-group can do it quickly: the nblk^2
+  // compares, in items of 64 blocks x 16 scores, come to at most 8 items per wave.  Otherwise a
+  // one-work-group rank launch (about 3 us) is cheaper than ranking in each work-group.
+  const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
+  if (nblk <= BSG_TOPK_MAX_NBLK && items <= 8 * (int64_t)pl.waves_per_group) {
+    // Two launches: the block scores, then the GEMM, whose work-groups each rank them and walk
+    // the kept list (work-group (0, 0) also publishes it).
+    rc = select_l1_launch(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream, false);
+    if (rc != BSG_OK) return rc;
+    const uint64_t* scores = (const uint64_t*)((const char*)ws + 256);
+    return launch_gemm(MODE_TOPK, x, ldx, bt, K, wp, N, nullptr, k, nullptr, nullptr, 0, y, ldy, dtype,
+                       (char*)ws + sel, ws_bytes - sel, &pl, stream, scores, idx_out, na_out);
+  }
+  rc = bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
+  if (rc != BSG_OK) return rc;
   return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, idx_out, kk, nullptr, nullptr, 0, y, ldy, dtype,
-                     (char*)ws + sel, ws_bytes - sel, plan, stream);
+                     (char*)ws + sel, ws_bytes - sel, &pl, stream);
 }
 
 }  // extern "C"
