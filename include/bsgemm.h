@@ -142,10 +142,11 @@ int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K,
                    void* y, int64_t ldy, int dtype,
                    void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
-/* Fused online block selector: score_j = sum_b sum_{c in block j} |x[b, 64j+c]| computed
- * exactly (integer units of 2^-24), top-k by (score desc, block id asc), compacted to an
- * ascending int32 list idx_out[min(k, nblk)] with the count written to *na_out (device).
- * One launch; the mask never round-trips to the host.  Replaces the torch op chain of
+/* Online block selector: score_j = sum_b sum_{c in block j} |x[b, 64j+c]| computed exactly
+ * (integer units of 2^-24), top-k by (score desc, block id asc), compacted to an ascending
+ * int32 list idx_out[min(k, nblk)] with the count written to *na_out (device).  Two launches
+ * on `stream` (block scores, then a one-work-group top-k); the mask never round-trips to the
+ * host.  The workspace needs no initialisation.  Replaces the torch op chain of
  * _select_active_blocks (scripts/bench_roundrobin_e2e_decode.py:90-113) with the L1 rule. */
 int64_t bsg_select_workspace_bytes(int64_t K);
 int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k,
@@ -179,10 +180,14 @@ typedef struct bsg_select_opts {
 int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
                     int32_t* idx_out, int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream);
 
-/* Selector followed by the GEMM on its device-side list, both on `stream`.
- * ws is split: the first bsg_select_workspace_bytes(K) bytes for the selector, the rest
- * (bsg_gemm_workspace_bytes) for the GEMM.  Replaces the select -> bitmap -> GEMM sequence
- * of _sparse_linear (scripts/bench_roundrobin_e2e_decode.py:179-284). */
+/* Selector followed by the GEMM on its device-side list, both on `stream`; idx_out and
+ * *na_out receive the kept list and count as from bsg_select_topk_l1.  Where the plan's waves
+ * can rank the scores quickly (nblk <= 512 and at most 8 items of 64 blocks x 16 scores per
+ * wave) every GEMM work-group ranks them itself and the call is two launches (scores, GEMM);
+ * otherwise three (scores, top-k, GEMM).  ws is split: the first bsg_select_workspace_bytes(K)
+ * bytes for the selector, the rest (bsg_gemm_workspace_bytes) for the GEMM.  Replaces the
+ * select -> bitmap -> GEMM sequence of _sparse_linear
+ * (scripts/bench_roundrobin_e2e_decode.py:179-284). */
 int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k,
                     const void* wp, int64_t N, int32_t* idx_out, int32_t* na_out,
                     void* y, int64_t ldy, int dtype,

@@ -9,9 +9,9 @@ kernels/shared_mask_batched_triton_min_runtime.py:4301):
     select(x_mlp)  -> gate/up GEMM (K=4096, N=2*11008)
     select(x_down) -> down GEMM  (K=11008, N=4096)
 
-Every select is the fused exact-L1 top-k kernel on that projection's input; its device-side list
-feeds the GEMM directly (no host round trip), so the whole step -- 32 layers x 4 x (select +
-GEMM) -- is one graph.  Attention, norms and activations are outside this path: the four inputs
+Every select is the exact-L1 top-k on that projection's input (a block-score launch, then the
+GEMM ranks the scores itself, or a rank launch precedes it); the list stays on the device (no
+host round trip), so the whole step -- 32 layers x 4 x (select + GEMM) -- is one graph.  Attention, norms and activations are outside this path: the four inputs
 of each layer are fixed synthetic activations, and weights are random with
 the Llama-2-7B architecture's shapes (~13 GB packed, resident in HBM).
 """
