@@ -142,6 +142,38 @@ int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K,
                    void* y, int64_t ldy, int dtype,
                    void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
+/* 2-D sparsity: only the active 64-column output blocks n_blocks[num_n] (device, ascending
+ * expected, block b = columns 64b .. 64b+63) are computed.  K-blocks as bsg_gemm
+ * (active_blocks[num_active], num_active_dev), or every K-block when both are NULL.
+ *   compact = 0 : Y [bt, N]; only the active blocks' columns are written, the rest untouched
+ *   compact = 1 : Y [bt, num_n * 64] (ldy >= num_n * 64); list entry i at columns 64i .. 64i+63,
+ *                 columns past N inside a block hold zeros
+ * num_n_dev (device, nullable) shortens the list below num_n with no host round trip; the
+ * tiles past it write nothing.  A block id outside [0, ceil(N/64)) reads no weights and writes
+ * nothing in place (zeros when compact).  num_n = 0 writes nothing.  The plan must cover at
+ * most 64 columns per work-group (cols_per_wave x column waves).  Workspace as bsg_gemm.
+ * Replaces _prepacked_block_sparse_gemm_2d_from_active_blocks (KRN:3498-3850) with its
+ * in-place (KRN:2289-2384) and compact (KRN:2473-2557) kernels. */
+int bsg_gemm_2d(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+                const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev,
+                const int32_t* n_blocks, int32_t num_n, const int32_t* num_n_dev, int compact,
+                void* y, int64_t ldy, int dtype,
+                void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
+/* Scatter a compact 2-D output back to the dense N axis:
+ * out[r, 64 n_blocks[i] + c] = compact[r, 64 i + c] for c < 64 and 64 n_blocks[i] + c < N,
+ * i < num_n (or *num_n_dev when set); other columns of out are untouched.  16-bit elements.
+ * Replaces _scatter_compact_to_dense_output (KRN:3470-3495), which loops on the host. */
+int bsg_scatter_nblocks(const void* compact, int64_t ldc, int64_t bt, const int32_t* n_blocks, int32_t num_n,
+                        const int32_t* num_n_dev, int64_t N, void* out, int64_t ldo, void* stream);
+
+/* Active 64-column output blocks of an element mask over N: the blocks b < ceil(N/64) with any
+ * mask[64b .. 64b+63] != 0, ascending, into n_blocks_out (room for ceil(N/64)), and their count
+ * into *num_out, both on the device.  Replaces the block-count state of
+ * _get_cached_active_n_blocks_delta (KRN:453-495); recomputed per call, so there is no delta
+ * state to keep. */
+int bsg_nmask_blocks(const uint8_t* mask, int64_t N, int32_t* n_blocks_out, int32_t* num_out, void* stream);
+
 /* Online block selector: score_j = sum_b sum_{c in block j} |x[b, 64j+c]| computed exactly
  * (integer units of 2^-24), top-k by (score desc, block id asc), compacted to an ascending
  * int32 list idx_out[min(k, nblk)] with the count written to *na_out (device).  Two launches

@@ -21,6 +21,10 @@ How each function is pinned (tests/test_oracle.py):
   select_topk_l1     brute-force sort by (-score, id); constructed ties; torch.topk on
                      CPU when scores are distinct
   n_keep             RRD:102 rounding (Python round) on the BASELINE pairs (0.52 -> 31/64)
+  gemm_2d_ref        every output block listed = gemm_ref (in place, and compact with the
+                     tail padded); pure-Python fp64 loop on tiny inputs with a partial last
+                     block and an out-of-range id; scatter_ref(compact) = in place
+  nmask_blocks_ref   brute force over reshaped masks (any per 64 columns)
 """
 from __future__ import annotations
 
@@ -103,6 +107,55 @@ def gemm_ref_torch(x_t, w_kn_t, idx_t):
 
     cols = (BLOCK_K * idx_t[:, None] + torch.arange(BLOCK_K)[None, :]).reshape(-1)
     return x_t.index_select(1, cols).float() @ w_kn_t.index_select(0, cols).float()
+
+
+BLOCK_N = 64  # KRN:19 INDEX_BLOCK_OUT_META_SIZE, the output-block width of the 2-D path
+
+
+def gemm_2d_ref(x: np.ndarray, w_nk: np.ndarray, k_idx, n_idx, out_init=None, compact: bool = False) -> np.ndarray:
+    """2-D block sparsity in fp32: Y = gemm_ref(x, w_nk, k_idx) restricted to the listed
+    64-column output blocks (KRN:2289-2384 in place, KRN:2473-2557 compact).  In place: a copy
+    of out_init [bt, N] with the listed blocks' columns (< N) replaced.  Compact: [bt, 64 *
+    len(n_idx)], entry i at columns 64i.. (columns past N zero).  A block id outside
+    [0, ceil(N/64)) writes nothing in place and zeros when compact (its weight columns are
+    masked off, KRN:2371-2375, 2544-2548)."""
+    y = gemm_ref(x, w_nk, k_idx)
+    bt, n = y.shape
+    nnb = (n + BLOCK_N - 1) // BLOCK_N
+    n_idx = np.asarray(n_idx, dtype=np.int64).reshape(-1)
+    if compact:
+        out = np.zeros((bt, BLOCK_N * len(n_idx)), dtype=np.float32)
+    else:
+        out = np.array(out_init, dtype=np.float32, copy=True)
+    for i, b in enumerate(n_idx):
+        if b < 0 or b >= nnb:
+            continue
+        c0, c1 = BLOCK_N * b, min(BLOCK_N * (b + 1), n)
+        if compact:
+            out[:, BLOCK_N * i:BLOCK_N * i + (c1 - c0)] = y[:, c0:c1]
+        else:
+            out[:, c0:c1] = y[:, c0:c1]
+    return out
+
+
+def scatter_ref(compact: np.ndarray, n_idx, out_init: np.ndarray) -> np.ndarray:
+    """out[:, 64 b_i + c] = compact[:, 64 i + c] for c < 64 and 64 b_i + c < N (KRN:3470-3495)."""
+    out = np.array(out_init, copy=True)
+    n = out.shape[1]
+    for i, b in enumerate(np.asarray(n_idx, dtype=np.int64).reshape(-1)):
+        if b < 0 or b >= (n + BLOCK_N - 1) // BLOCK_N:
+            continue
+        w = min(BLOCK_N, n - BLOCK_N * b)
+        out[:, BLOCK_N * b:BLOCK_N * b + w] = compact[:, BLOCK_N * i:BLOCK_N * i + w]
+    return out
+
+
+def nmask_blocks_ref(mask: np.ndarray, n: int) -> np.ndarray:
+    """Ascending ids of the 64-column blocks with any nonzero mask entry below N (the block
+    counts of KRN:453-495 taken > 0)."""
+    m = np.asarray(mask).reshape(-1)[:n] != 0
+    return np.array([b for b in range((n + BLOCK_N - 1) // BLOCK_N) if m[BLOCK_N * b:BLOCK_N * (b + 1)].any()],
+                    dtype=np.int32)
 
 
 def bitmap_from_list(idx, total_k_blocks: int) -> np.ndarray:

@@ -127,6 +127,35 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert "workspace" in _lib.last_error() or "K" in _lib.last_error()
 
 
+def test_2d_entry_points_reject_bad_arguments_without_launching():
+    lib = bsa.load()
+    p = _lib.Plan(1, 16, 2, 4, 16, 1)
+    ok = dict(x=FAKE, ldx=4096, bt=16, K=4096, wp=FAKE, N=4096, idx=FAKE, na=10, nad=None, nb=FAKE, nn=3, nnd=None,
+              compact=0, y=FAKE, ldy=4096, dtype=0, ws=None, ws_bytes=0, plan=p)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.bsg_gemm_2d(a["x"], a["ldx"], a["bt"], a["K"], a["wp"], a["N"], a["idx"], a["na"], a["nad"],
+                               a["nb"], a["nn"], a["nnd"], a["compact"], a["y"], a["ldy"], a["dtype"], a["ws"],
+                               a["ws_bytes"], ctypes.byref(a["plan"]), None)
+
+    assert call(nn=65) == _lib.BSG_ERR_ARG           # more blocks than ceil(N/64)
+    assert call(nn=-1) == _lib.BSG_ERR_ARG
+    assert call(nb=None) == _lib.BSG_ERR_ARG
+    assert call(compact=1, ldy=100) == _lib.BSG_ERR_ARG  # compact Y needs nn * 64 columns
+    assert call(ldy=100) == _lib.BSG_ERR_ARG             # in place needs N
+    assert call(nn=0, nb=None) == _lib.BSG_OK            # no output block: nothing to launch
+    wide = _lib.Plan(1, 32, 4, 4, 32, 2)                 # 128 columns per work-group
+    assert call(plan=wide) == _lib.BSG_ERR_UNSUPPORTED
+    assert "64" in _lib.last_error()
+    assert lib.bsg_scatter_nblocks(FAKE, 100, 16, FAKE, 2, None, 4096, FAKE, 4096, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_scatter_nblocks(FAKE, 4096, 16, FAKE, 65, None, 4096, FAKE, 4096, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_scatter_nblocks(FAKE, 128, 16, FAKE, 2, None, 4096, FAKE, 100, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_scatter_nblocks(FAKE, 128, 16, FAKE, 0, None, 4096, FAKE, 4096, None) == _lib.BSG_OK
+    assert lib.bsg_nmask_blocks(FAKE, 0, FAKE, FAKE, None) == _lib.BSG_ERR_ARG
+    assert lib.bsg_nmask_blocks(None, 64, FAKE, FAKE, None) == _lib.BSG_ERR_ARG
+
+
 def test_bitmap_and_select_reject_bad_arguments():
     lib = bsa.load()
     p = _lib.Plan(1, 32, 4, 4, 16, 1)

@@ -234,3 +234,58 @@ def test_perstep_fixture_matches_reference_summaries():
         sel = f["batch"] == b
         assert sel.sum() == 55 and abs(f["ref_step_speedup"][sel].mean() - s) < 1e-12
     assert [round(float(v), 3) for v in f["ref_batch_speedup"]] == [1.948, 1.945, 1.761, 1.602, 1.405, 1.203]
+
+
+def test_gemm_2d_every_block_is_the_1d_gemm():
+    rng = np.random.default_rng(21)
+    bt, k, n = 3, 200, 150  # partial last K-block and output block
+    x = rng.normal(size=(bt, k)).astype(np.float16)
+    w = rng.normal(size=(n, k)).astype(np.float16)
+    kb = [0, 2, 3]
+    y = orc.gemm_ref(x, w, kb)
+    allb = list(range(3))
+    np.testing.assert_array_equal(orc.gemm_2d_ref(x, w, kb, allb, out_init=np.zeros((bt, n))), y)
+    c = orc.gemm_2d_ref(x, w, kb, allb, compact=True)
+    assert c.shape == (bt, 192)
+    np.testing.assert_array_equal(c[:, :n], y)
+    assert not np.any(c[:, n:])
+
+
+def test_gemm_2d_brute_force_loops():
+    """Pure-Python fp64 loops: a partial last output block, an unsorted list and an id past
+    the last block (nothing in place, zeros when compact)."""
+    rng = np.random.default_rng(22)
+    bt, k, n = 2, 128, 130
+    x = rng.normal(size=(bt, k)).astype(np.float16)
+    w = rng.normal(size=(n, k)).astype(np.float16)
+    kb, nb = [1], [2, 0, 7]
+    init = np.full((bt, n), 5.0, dtype=np.float32)
+    want = init.astype(np.float64).copy()
+    wantc = np.zeros((bt, 64 * len(nb)))
+    for r in range(bt):
+        for i, b in enumerate(nb):
+            for c in range(64):
+                col = 64 * b + c
+                if b > 2 or col >= n:
+                    continue
+                s = 0.0
+                for j in kb:
+                    for ch in range(64 * j, 64 * j + 64):
+                        s += float(x[r, ch]) * float(w[col, ch])
+                want[r, col] = s
+                wantc[r, 64 * i + c] = s
+    got = orc.gemm_2d_ref(x, w, kb, nb, out_init=init)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(orc.gemm_2d_ref(x, w, kb, nb, compact=True), wantc, rtol=1e-5, atol=1e-4)
+    # the compact result scattered back is the in-place result
+    comp = orc.gemm_2d_ref(x, w, kb, nb, compact=True)
+    np.testing.assert_array_equal(orc.scatter_ref(comp, nb, init), got)
+
+
+def test_nmask_blocks_brute_force():
+    rng = np.random.default_rng(23)
+    for n in (1, 64, 65, 1000, 4096):
+        m = (rng.random(n) < 0.01).astype(np.uint8)
+        want = [b for b in range((n + 63) // 64) if any(m[c] for c in range(64 * b, min(64 * b + 64, n)))]
+        np.testing.assert_array_equal(orc.nmask_blocks_ref(m, n), np.array(want, dtype=np.int32))
+    assert orc.nmask_blocks_ref(np.zeros(300, np.uint8), 300).size == 0

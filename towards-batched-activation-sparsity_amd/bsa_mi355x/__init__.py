@@ -19,6 +19,11 @@ from .runtime import (INDEX_BLOCK_META_SIZE, TileConfig, _build_active_k_bitmap,
                       resolve_plan)
 from .select import (_energy_expanded_active_blocks, _select_active_blocks, _select_active_blocks_l1,
                      _topk_energy_ratio, select_sparse_gemm, select_topk, select_topk_l1)
+from .sparse2d import (INDEX_BLOCK_OUT_META_SIZE, _get_cached_active_n_blocks_delta,
+                       _prepacked_block_sparse_gemm_2d_bitmap_from_active_blocks,
+                       _prepacked_block_sparse_gemm_2d_compact_from_active_blocks,
+                       _prepacked_block_sparse_gemm_2d_from_active_blocks, _scatter_compact_to_dense_output,
+                       gemm_2d_packed, nmask_blocks, scatter_nblocks)
 
 __all__ = [
     "BLOCK_K", "MAX_NBLK", "INDEX_BLOCK_META_SIZE", "Plan", "TileConfig", "load",
@@ -33,4 +38,8 @@ __all__ = [
     "release_prepacked_weights", "n_keep_for_density", "active_bytes", "nblk_of",
     "select_topk_l1", "select_topk", "select_sparse_gemm", "_select_active_blocks_l1", "_select_active_blocks",
     "_topk_energy_ratio", "_energy_expanded_active_blocks",
+    "INDEX_BLOCK_OUT_META_SIZE", "_prepacked_block_sparse_gemm_2d_from_active_blocks",
+    "_prepacked_block_sparse_gemm_2d_bitmap_from_active_blocks",
+    "_prepacked_block_sparse_gemm_2d_compact_from_active_blocks", "_scatter_compact_to_dense_output",
+    "_get_cached_active_n_blocks_delta", "gemm_2d_packed", "scatter_nblocks", "nmask_blocks",
 ]

@@ -112,6 +112,10 @@ SIGNATURES = {
     "bsg_gemm": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_gemm_bitmap": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_gemm_dense": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
+    "bsg_gemm_2d": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _int, _vp, _i64, _int,
+                           _vp, _i64, _pplan, _vp]),
+    "bsg_scatter_nblocks": (_int, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _vp]),
+    "bsg_nmask_blocks": (_int, [_vp, _i64, _vp, _vp, _vp]),
     "bsg_select_workspace_bytes": (_i64, [_i64]),
     "bsg_select_topk_l1": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _int, _vp, _i64, _vp]),
     "bsg_select_topk": (_int, [_vp, _i64, _i64, _i64, _i32, ctypes.POINTER(SelectOpts), _vp, _vp, _int, _vp,

@@ -312,6 +312,12 @@ struct GemmParams {
   int32_t* idx_out;
   int32_t* na_out;
   int32_t keyed;
+  // 2-D sparsity: ascending active 64-column output blocks (null: every column), their count
+  // (host value, or the device one when nn_dev is set), whether Y is compact (active blocks
+  // side by side), and the width Y stores are bounded by (N, or nn * 64 when compact)
+  const int32_t* nidx;
+  const int32_t* nn_dev;
+  int32_t nn, ncompact, ny;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -325,6 +331,35 @@ __device__ __forceinline__ void tile_of_group(int split_k, int* tile, int* sk) {
   const int lid = (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
   *tile = lid / split_k;
   *sk = lid - *tile * split_k;
+}
+
+// Columns of column tile `tile` (gc columns wide): n0 = first weight column it reads, n0y =
+// first output column it writes.  N2D (2-D sparsity, a separate instantiation so the 1-D
+// kernels carry none of it): tile t is piece t % (64/gc) of active 64-column block
+// nidx[t / (64/gc)]; compact output packs the active blocks side by side.  Returns false when
+// the tile has no block (past the device-side count): the whole work-group then returns
+// before any barrier.  A block id outside [0, ceil(N/64)) reads past the packed columns (zero
+// weights) and writes nothing.
+template <bool N2D>
+__device__ __forceinline__ bool tile_columns(const GemmParams& p, int tile, int gc, int* n0, int* n0y) {
+  if constexpr (!N2D) {
+    *n0 = *n0y = tile * gc;
+    return true;
+  }
+  const int per = 64 / gc;
+  const int bi = tile / per;
+  int nn = p.nn;
+  if (p.nn_dev != nullptr) {
+    const int d = __builtin_amdgcn_readfirstlane(*p.nn_dev);
+    nn = d < 0 ? 0 : (d < nn ? d : nn);
+  }
+  if (bi >= nn) return false;
+  const int off = (tile - bi * per) * gc;
+  const int nb = __builtin_amdgcn_readfirstlane(p.nidx[bi]);
+  const bool ok = nb >= 0 && nb < (p.N + 63) / 64;
+  *n0 = ok ? nb * 64 + off : p.npad;
+  *n0y = p.ncompact ? bi * 64 + off : (ok ? *n0 : p.ny);
+  return true;
 }
 
 // Stage this call's active-block list in LDS (list copy, bitmap compaction, top-k of block
@@ -383,17 +418,17 @@ __device__ __forceinline__ void store_y(const GemmParams& p, int y0, int n0, int
   if (b >= p.bt) return;
   uint16_t* yrow = (uint16_t*)p.y + (size_t)b * (size_t)p.ldy;
   if (p.y_fast) {
-    if (n < p.N) {
+    if (n < p.ny) {
       u32x2 pk;
       pk.x = (uint32_t)Elem<T>::bits(v.x) | ((uint32_t)Elem<T>::bits(v.y) << 16);
       pk.y = (uint32_t)Elem<T>::bits(v.z) | ((uint32_t)Elem<T>::bits(v.w) << 16);
       *(u32x2*)(yrow + n) = pk;
     }
   } else {
-    if (n + 0 < p.N) yrow[n + 0] = Elem<T>::bits(v.x);
-    if (n + 1 < p.N) yrow[n + 1] = Elem<T>::bits(v.y);
-    if (n + 2 < p.N) yrow[n + 2] = Elem<T>::bits(v.z);
-    if (n + 3 < p.N) yrow[n + 3] = Elem<T>::bits(v.w);
+    if (n + 0 < p.ny) yrow[n + 0] = Elem<T>::bits(v.x);
+    if (n + 1 < p.ny) yrow[n + 1] = Elem<T>::bits(v.y);
+    if (n + 2 < p.ny) yrow[n + 2] = Elem<T>::bits(v.z);
+    if (n + 3 < p.ny) yrow[n + 3] = Elem<T>::bits(v.w);
   }
 }
 
@@ -465,7 +500,7 @@ __device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_l
 // the work-group's share of the block list into contiguous slices and are reduced through LDS
 // in wave order.  Each wave loads its own X fragments.  Best when bt is small (the X fragments
 // are few) and many narrow column tiles are needed to fill the chip.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH>
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
   constexpr int F = BTT * NSUB;
@@ -482,7 +517,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   int tile, sk;
   tile_of_group(p.split_k, &tile, &sk);
   const int S = p.split_k;
-  const int n0 = tile * (16 * NSUB);
+  int n0, n0y;
+  if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
   const int y0 = blockIdx.y * (16 * BTT);
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
@@ -563,7 +599,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
   auto emit = [&](int f, f32x4 v) {
     if (S == 1)
-      store_y<T, NSUB>(p, y0, n0, f, v);
+      store_y<T, NSUB>(p, y0, n0y, f, v);
     else
       part_emit<F>(p, tile_lin, sk, f, v);
   };
@@ -596,7 +632,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
   }
 
-  if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
+  if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
 }
 
 // Kinds 2 and 4 ("xlds"): one work-group = BTT*16 batch rows x WC*NSUB*16 columns; its waves
@@ -607,7 +643,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
 // (WK = 2): 2*WC waves, column group x 32-channel half of every block, so each wave issues half
 // the MFMAs and LDS reads of a block and two waves share each SIMD, overlapping one wave's
 // barrier and LDS waits with the other's MFMAs; the halves are summed through LDS at the end.
-template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH>
+template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D>
 __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p) {
   constexpr int WPG = WC * WK;
   constexpr int NT = 64 * WPG;
@@ -628,7 +664,8 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   int tile, sk;
   tile_of_group(p.split_k, &tile, &sk);
   const int S = p.split_k;
-  const int n0 = tile * (16 * CS);
+  int n0, n0y;
+  if (!tile_columns<N2D>(p, tile, 16 * CS, &n0, &n0y)) return;
   const int y0 = blockIdx.y * (16 * BTT);
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
@@ -733,12 +770,12 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
       for (int s = 0; s < NSUB; ++s) {
         const int g = bi * CS + wc * NSUB + s;
         if (S == 1)
-          store_y<T, CS>(p, y0, n0, g, acc[bi][s]);
+          store_y<T, CS>(p, y0, n0y, g, acc[bi][s]);
         else
           part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
       }
   }
-  if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0, w, &s_misc[WPG]);
+  if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
 }
 
 // Kind 3 ("fma", batch tiles of 1-8 rows): the contraction is too thin for MFMA, so each lane
@@ -750,7 +787,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
 // [block][row][half h][group g] 16-byte order, so each of those reads is a broadcast; the loop
 // then streams weights only.  The waves split the work-group's block list (as kind 1) and are
 // reduced through LDS in wave order.
-template <typename T, int BT, int NSUB, int WPG, int DEPTH>
+template <typename T, int BT, int NSUB, int WPG, int DEPTH, bool N2D>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
   constexpr int XI = BSG_FMA_X_LOADS;  // staging loads per wave (host guarantees enough)
@@ -762,7 +799,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = blockIdx.x;
-  const int n0 = tile * (16 * NSUB);
+  int n0, n0y;
+  if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
   const int y0 = blockIdx.y * BT;
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
@@ -782,7 +820,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     qid[i] = s_ids[q < na ? q : 0];
   }
   const int blk_bytes = p.npad * 128;
-  const int wcol = lane * 16 + tile * NSUB * 2048;
+  const int wcol = lane * 16 + (n0 >> 4) * 2048;
   u32x4 wv[DEPTH][NSUB][2];
   float acc[NSUB][BT];
 #pragma unroll
@@ -890,13 +928,13 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   if (w == 0 && lane < 16) {
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      const int n = n0 + 16 * s + lane;
+      const int n = n0y + 16 * s + lane;
 #pragma unroll
       for (int b = 0; b < BT; ++b) {
         float v = acc[s][b];
         for (int ww = 1; ww < WPG; ++ww) v += s_red[ww - 1][s * BT + b][lane];
         const int row = y0 + b;
-        if (row < p.bt && n < p.N) ((uint16_t*)p.y)[(size_t)row * (size_t)p.ldy + n] = Elem<T>::bits(v);
+        if (row < p.bt && n < p.ny) ((uint16_t*)p.y)[(size_t)row * (size_t)p.ldy + n] = Elem<T>::bits(v);
       }
     }
   }
@@ -1204,24 +1242,94 @@ __global__ __launch_bounds__(1024) void bsg_rank_l1_kernel(SelParams p) {
 // ----------------------------------------------------------------------------------------
 // Host side: kernel table, plan resolution, validation, launches.
 
+// Compact 2-D output back to the dense N axis: work-group i copies active block i (64 columns,
+// 256 threads = 4 rows x 64 columns per step) to columns 64 * n_blocks[i] .. (below N).
+__global__ __launch_bounds__(256) void bsg_scatter_kernel(const uint16_t* __restrict__ c, int64_t ldc, int32_t bt,
+                                                          const int32_t* __restrict__ nb, int32_t nn,
+                                                          const int32_t* __restrict__ nn_dev, int32_t N,
+                                                          uint16_t* __restrict__ out, int64_t ldo) {
+  const int i = blockIdx.x;
+  int cnt = nn;
+  if (nn_dev != nullptr) {
+    const int d = *nn_dev;
+    cnt = d < 0 ? 0 : (d < nn ? d : nn);
+  }
+  if (i >= cnt) return;
+  const int b = nb[i];
+  if (b < 0 || b >= (N + 63) / 64) return;
+  const int col = threadIdx.x & 63;
+  const int dst = 64 * b + col;
+  if (dst >= N) return;
+  for (int r = blockIdx.y * 4 + (threadIdx.x >> 6); r < bt; r += gridDim.y * 4)
+    out[(size_t)r * (size_t)ldo + dst] = c[(size_t)r * (size_t)ldc + 64 * i + col];
+}
+
+// Active 64-column blocks of an element mask (any byte != 0), ascending, with their count: one
+// work-group walks the blocks 1024 at a time, each thread testing one block, and compacts the
+// flags with a work-group scan.
+__global__ __launch_bounds__(1024) void bsg_nmask_kernel(const uint8_t* __restrict__ mask, int64_t N,
+                                                         int32_t* __restrict__ out, int32_t* __restrict__ count) {
+  __shared__ int s_scan[16];
+  const int tid = threadIdx.x;
+  const int64_t nb = (N + 63) / 64;
+  int base = 0;
+  for (int64_t b0 = 0; b0 < nb; b0 += 1024) {
+    const int64_t b = b0 + tid;
+    int any = 0;
+    if (b < nb) {
+      const int64_t e = 64 * b + 64 < N ? 64 * b + 64 : N;
+      for (int64_t c = 64 * b; c < e; ++c) any |= mask[c];
+    }
+    int total = 0;
+    const int o = wg_exclusive_scan<1024>(any != 0, s_scan, &total);
+    if (any != 0) out[base + o] = (int32_t)b;
+    base += total;
+  }
+  if (tid == 0) *count = base;
+}
+
 typedef void (*GemmFn)(GemmParams);
 
 enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4 };
 
+// 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
 struct KernelEntry {
   int kind, rows, nsub, wpg, depth;
-  GemmFn f16, bf16;
+  GemmFn f16, bf16, f16_2d, bf16_2d;
 };
 
-#define BSG_K(B, S, W, D) \
-  {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D>, bsg_gemm_kernel<__bf16, B, S, W, D>}
-#define BSG_X(B, S, W, D) \
-  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D>, bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D>}
-#define BSG_Y(B, S, W, D)                                                             \
-  {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D>, \
-   bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D>}
-#define BSG_F(R, S, W, D) \
-  {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D>, bsg_gemm_fma_kernel<__bf16, R, S, W, D>}
+// The 2-D instantiation of a tile, or null when its work-group covers more than one 64-column
+// output block (the discarded branch is never instantiated).
+template <int KIND, typename T, int B, int S, int W, int D>
+constexpr GemmFn kernel_2d() {
+  constexpr int gc = KIND == KIND_XLDS ? 16 * S * W : (KIND == KIND_XLDS_KH ? 16 * S * (W / 2) : 16 * S);
+  if constexpr (gc > 64) {
+    return nullptr;
+  } else if constexpr (KIND == KIND_KSPLIT) {
+    return bsg_gemm_kernel<T, B, S, W, D, true>;
+  } else if constexpr (KIND == KIND_XLDS) {
+    return bsg_gemm_xl_kernel<T, B, S, W, 1, D, true>;
+  } else if constexpr (KIND == KIND_XLDS_KH) {
+    return bsg_gemm_xl_kernel<T, B, S, W / 2, 2, D, true>;
+  } else {
+    return bsg_gemm_fma_kernel<T, B, S, W, D, true>;
+  }
+}
+
+#define BSG_K(B, S, W, D)                                                                                          \
+  {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D, false>, bsg_gemm_kernel<__bf16, B, S, W, D, false>, \
+   kernel_2d<KIND_KSPLIT, _Float16, B, S, W, D>(), kernel_2d<KIND_KSPLIT, __bf16, B, S, W, D>()}
+#define BSG_X(B, S, W, D)                                                                     \
+  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false>,           \
+   bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D, false>, kernel_2d<KIND_XLDS, _Float16, B, S, W, D>(), \
+   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>()}
+#define BSG_Y(B, S, W, D)                                                                        \
+  {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false>,        \
+   bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D, false>, kernel_2d<KIND_XLDS_KH, _Float16, B, S, W, D>(), \
+   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>()}
+#define BSG_F(R, S, W, D)                                                                                 \
+  {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
+   kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>()}
 
 // Instantiated tile set.  Kind 1 registers per lane ~ depth*(nsub+btt)*8 + btt*nsub*4;
 // kind 2 ~ depth*(nsub*8 + ceil(2*btt/wpg)*4) + btt*nsub*4.
@@ -1397,7 +1505,10 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
 
 int64_t gemm_ws_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
   if (pl->split_k <= 1) return 0;
-  const int64_t n_tiles = cdiv(cdiv(N, 16) * 16, group_cols(pl));
+  // enough for the 1-D tiling and for a 2-D launch over every 64-column block
+  const int64_t gc = group_cols(pl);
+  int64_t n_tiles = cdiv(cdiv(N, 16) * 16, gc);
+  if (gc <= 64 && cdiv(N, 64) * (64 / gc) > n_tiles) n_tiles = cdiv(N, 64) * (64 / gc);
   const int64_t tiles = n_tiles * cdiv(bt, pl->rows_per_group);
   const int64_t frag = (int64_t)(pl->rows_per_group / 16) * (group_cols(pl) / 16);
   const int64_t part = tiles * pl->split_k * frag * 64 * 16;
@@ -1420,8 +1531,9 @@ int device_cu_count() {
   return cache[dev];
 }
 
+// y_cols: the columns Y must hold (N, or the compact width of a 2-D launch).
 int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
-                 void* y, int64_t ldy, int dtype) {
+                 void* y, int64_t ldy, int dtype, int64_t y_cols) {
   if (dtype != BSG_F16 && dtype != BSG_BF16) return fail(BSG_ERR_DTYPE, "dtype=%d (0=fp16, 1=bf16)", dtype);
   if (bt < 0 || K <= 0 || N <= 0) return fail(BSG_ERR_ARG, "sizes bt=%lld K=%lld N=%lld", (long long)bt, (long long)K, (long long)N);
   if (cdiv(K, BSG_BLOCK_K) > BSG_MAX_NBLK)
@@ -1432,7 +1544,7 @@ int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* 
   if (ldx < K || ldx % 8 != 0 || !aligned16(x))
     return fail(BSG_ERR_ALIGN, "x must be 16-byte aligned with ldx >= K and ldx %% 8 == 0 (ldx=%lld)", (long long)ldx);
   if (!aligned16(wp)) return fail(BSG_ERR_ALIGN, "packed weight must be 16-byte aligned");
-  if (ldy < N) return fail(BSG_ERR_ARG, "ldy=%lld < N=%lld", (long long)ldy, (long long)N);
+  if (ldy < y_cols) return fail(BSG_ERR_ARG, "ldy=%lld < %lld output columns", (long long)ldy, (long long)y_cols);
   if (((uintptr_t)y & 1u) != 0) return fail(BSG_ERR_ALIGN, "y must be 2-byte aligned");
   if ((bt - 1) * ldx * 2 + ldx * 2 >= (int64_t)0x7fffffff)
     return fail(BSG_ERR_UNSUPPORTED, "x spans >= 2 GiB");
@@ -1440,21 +1552,37 @@ int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* 
   return BSG_OK;
 }
 
-// MODE_TOPK: na is k, scores the exact-L1 block scores; the kept list and its count are
-// published to idx_out / na_out (when not null) by work-group (0, 0).
+// Optional parts of a launch.  MODE_TOPK: the exact-L1 block scores (na is then k), and where
+// work-group (0, 0) publishes the kept list and its count (null: not published).  2-D
+// sparsity: the active 64-column output blocks nidx[nn] (device; nn_dev, when set, a device
+// count <= nn), and whether Y is compact ([bt, nn * 64], the blocks side by side).
+struct LaunchExtras {
+  const uint64_t* scores = nullptr;
+  int32_t* idx_out = nullptr;
+  int32_t* na_out = nullptr;
+  const int32_t* nidx = nullptr;
+  int32_t nn = 0;
+  const int32_t* nn_dev = nullptr;
+  int ncompact = 0;
+};
+
 int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp,
                 int64_t N, const int32_t* idx, int32_t na, const int32_t* na_dev,
                 const uint8_t* bitmap, int32_t nbm, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
-                const bsg_plan* plan_in, void* stream, const uint64_t* scores = nullptr,
-                int32_t* idx_out = nullptr, int32_t* na_out = nullptr) {
-  int rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype);
+                const bsg_plan* plan_in, void* stream, const LaunchExtras& ex = LaunchExtras{}) {
+  const int64_t n_blocks = cdiv(N, 64);
+  if (ex.nidx != nullptr && (ex.nn < 0 || ex.nn > n_blocks))
+    return fail(BSG_ERR_ARG, "2-D: %d active output blocks (0..%lld)", ex.nn, (long long)n_blocks);
+  const int64_t y_cols = ex.nidx != nullptr && ex.ncompact ? (int64_t)ex.nn * 64 : N;
+  int rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype, y_cols);
   if (rc != BSG_OK || bt == 0) return rc;
+  if (ex.nidx != nullptr && ex.nn == 0) return BSG_OK;  // no output block: nothing to write
   const int32_t nblk = (int32_t)cdiv(K, BSG_BLOCK_K);
   if (mode == MODE_LIST) {
     if (na < 0 || na > BSG_MAX_NBLK) return fail(BSG_ERR_ARG, "num_active=%d (0..%d)", na, BSG_MAX_NBLK);
     if (na > 0 && !idx) return fail(BSG_ERR_ARG, "active_blocks is null");
   } else if (mode == MODE_TOPK) {
-    if (!scores || na < 0) return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)scores, na);
+    if (!ex.scores || na < 0) return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)ex.scores, na);
     if (nblk > BSG_TOPK_MAX_NBLK)
       return fail(BSG_ERR_UNSUPPORTED, "top-k in the GEMM: %d blocks (at most %d)", nblk, BSG_TOPK_MAX_NBLK);
     if (na > nblk) na = nblk;
@@ -1469,7 +1597,8 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   bsg_plan pl = plan_in ? *plan_in : bsg_plan{0, 0, 0, 0, 0, 0};
   int cu = 256;
   if (pl.split_k == 0) cu = device_cu_count();  // only feeds the automatic split-K choice
-  rc = resolve(bt, N, nblk, na, cu, &pl);
+  // a 2-D launch fills the chip with its active blocks only
+  rc = resolve(bt, ex.nidx != nullptr ? (int64_t)ex.nn * 64 : N, nblk, na, cu, &pl);
   if (rc != BSG_OK) return rc;
   const int64_t need = gemm_ws_bytes(bt, N, &pl);
   if (need > 0 && !aligned16(ws)) return fail(BSG_ERR_ALIGN, "workspace must be 16-byte aligned");
@@ -1479,7 +1608,12 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   const KernelEntry* ke =
       find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
   const int64_t npad = cdiv(N, 16) * 16;
-  const int64_t n_tiles = cdiv(npad, group_cols(&pl));
+  const int64_t gc = group_cols(&pl);
+  if (ex.nidx != nullptr && gc > 64)
+    return fail(BSG_ERR_UNSUPPORTED, "2-D: the plan covers %lld columns per work-group (at most 64: "
+                "cols_per_wave x column waves)", (long long)gc);
+  // 2-D: 64 / gc tiles per active output block (a device-side count leaves tiles idle)
+  const int64_t n_tiles = ex.nidx != nullptr ? (int64_t)ex.nn * (64 / gc) : cdiv(npad, gc);
   const int64_t ygroups = cdiv(bt, pl.rows_per_group);
   if (n_tiles * pl.split_k > 0x7fffffff || ygroups > 65535) return fail(BSG_ERR_UNSUPPORTED, "grid too large");
 
@@ -1507,15 +1641,21 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.split_k = pl.split_k;
   p.n_tiles = (int32_t)n_tiles;
   p.x_bytes = (int32_t)(((bt - 1) * ldx + K) * 2);
-  p.y_fast = (N % 4 == 0) && (ldy % 4 == 0) && (((uintptr_t)y & 7u) == 0);
-  p.scores = scores;
-  p.idx_out = idx_out;
-  p.na_out = na_out;
+  p.ny = (int32_t)y_cols;
+  p.y_fast = (y_cols % 4 == 0) && (ldy % 4 == 0) && (((uintptr_t)y & 7u) == 0);
+  p.scores = ex.scores;
+  p.idx_out = ex.idx_out;
+  p.na_out = ex.na_out;
   p.keyed = bt <= 64;
+  p.nidx = ex.nidx;
+  p.nn_dev = ex.nn_dev;
+  p.nn = ex.nn;
+  p.ncompact = ex.ncompact;
 
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
-  GemmFn fn = dtype == BSG_F16 ? ke->f16 : ke->bf16;
+  GemmFn fn = ex.nidx != nullptr ? (dtype == BSG_F16 ? ke->f16_2d : ke->bf16_2d) : (dtype == BSG_F16 ? ke->f16 : ke->bf16);
+  if (fn == nullptr) return fail(BSG_ERR_UNSUPPORTED, "2-D: no instantiation for this tile");
   // Kind 3: LDS for the staged activations of the whole list (na is the list capacity; a
   // device-side count or a bitmap only shortens it).
   const size_t dyn_lds = pl.kind == KIND_FMA ? (size_t)na * (size_t)pl.rows_per_group * 128 : 0;
@@ -1601,6 +1741,54 @@ int bsg_gemm_dense(const void* x, int64_t ldx, int64_t bt, int64_t K, const void
                    int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
   return launch_gemm(MODE_DENSE, x, ldx, bt, K, wp, N, nullptr, 0, nullptr, nullptr, 0, y, ldy, dtype, ws,
                      ws_bytes, plan, stream);
+}
+
+int bsg_gemm_2d(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+                const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev,
+                const int32_t* n_blocks, int32_t num_n, const int32_t* num_n_dev, int compact, void* y,
+                int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  if (num_n < 0 || num_n > cdiv(N, 64))
+    return fail(BSG_ERR_ARG, "2-D: num_n=%d outside [0, ceil(N/64)] (N=%lld)", num_n, (long long)N);
+  if (num_n == 0)  // no output block: only the checks run, nothing is written
+    return check_common(x, ldx, bt, K, wp, N, y, ldy, dtype, compact ? 0 : N);
+  if (!n_blocks) return fail(BSG_ERR_ARG, "2-D: n_blocks is null");
+  LaunchExtras ex;
+  ex.nidx = n_blocks;
+  ex.nn = num_n;
+  ex.nn_dev = num_n_dev;
+  ex.ncompact = compact != 0;
+  if (active_blocks == nullptr && num_active_dev == nullptr)
+    return launch_gemm(MODE_DENSE, x, ldx, bt, K, wp, N, nullptr, 0, nullptr, nullptr, 0, y, ldy, dtype, ws,
+                       ws_bytes, plan, stream, ex);
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, active_blocks, num_active, num_active_dev, nullptr, 0, y,
+                     ldy, dtype, ws, ws_bytes, plan, stream, ex);
+}
+
+int bsg_scatter_nblocks(const void* compact, int64_t ldc, int64_t bt, const int32_t* n_blocks, int32_t num_n,
+                        const int32_t* num_n_dev, int64_t N, void* out, int64_t ldo, void* stream) {
+  if (bt < 0 || N <= 0 || num_n < 0 || num_n > cdiv(N, 64) || N > 0x7fffffff)
+    return fail(BSG_ERR_ARG, "scatter: bt=%lld N=%lld num_n=%d", (long long)bt, (long long)N, num_n);
+  if (bt == 0 || num_n == 0) return BSG_OK;
+  if (!compact || !n_blocks || !out) return fail(BSG_ERR_ARG, "scatter: null pointer");
+  if (ldc < (int64_t)num_n * 64 || ldo < N)
+    return fail(BSG_ERR_ARG, "scatter: ldc=%lld (>= %d) ldo=%lld (>= N)", (long long)ldc, num_n * 64, (long long)ldo);
+  if (((uintptr_t)compact & 1u) || ((uintptr_t)out & 1u)) return fail(BSG_ERR_ALIGN, "scatter: 2-byte alignment");
+  const int64_t gy = cdiv(bt, 4) < 64 ? cdiv(bt, 4) : 64;
+  hipLaunchKernelGGL(bsg_scatter_kernel, dim3((unsigned)num_n, (unsigned)gy), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)compact, ldc, (int32_t)bt, n_blocks, num_n, num_n_dev, (int32_t)N,
+                     (uint16_t*)out, ldo);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_scatter_nblocks launch");
+  return BSG_OK;
+}
+
+int bsg_nmask_blocks(const uint8_t* mask, int64_t N, int32_t* n_blocks_out, int32_t* num_out, void* stream) {
+  if (N <= 0 || N > 0x7fffffff) return fail(BSG_ERR_ARG, "nmask: N=%lld", (long long)N);
+  if (!mask || !n_blocks_out || !num_out) return fail(BSG_ERR_ARG, "nmask: null pointer");
+  hipLaunchKernelGGL(bsg_nmask_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, mask, N, n_blocks_out, num_out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "bsg_nmask_blocks launch");
+  return BSG_OK;
 }
 
 int64_t bsg_select_workspace_bytes(int64_t K) {
@@ -1748,8 +1936,12 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
     rc = select_l1_launch(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream, false);
     if (rc != BSG_OK) return rc;
     const uint64_t* scores = (const uint64_t*)((const char*)ws + 256);
+    LaunchExtras ex;
+    ex.scores = scores;
+    ex.idx_out = idx_out;
+    ex.na_out = na_out;
     return launch_gemm(MODE_TOPK, x, ldx, bt, K, wp, N, nullptr, k, nullptr, nullptr, 0, y, ldy, dtype,
-                       (char*)ws + sel, ws_bytes - sel, &pl, stream, scores, idx_out, na_out);
+                       (char*)ws + sel, ws_bytes - sel, &pl, stream, ex);
   }
   rc = bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
   if (rc != BSG_OK) return rc;

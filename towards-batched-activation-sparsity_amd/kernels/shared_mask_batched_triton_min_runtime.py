@@ -22,6 +22,14 @@ from bsa_mi355x.runtime import (  # noqa: F401
     prepacked_block_sparse_gemm_bitmap_preload_batched_kernel,
 )
 from bsa_mi355x.select import _select_active_blocks_l1  # noqa: F401
+from bsa_mi355x.sparse2d import (  # noqa: F401
+    INDEX_BLOCK_OUT_META_SIZE,
+    _get_cached_active_n_blocks_delta,
+    _prepacked_block_sparse_gemm_2d_bitmap_from_active_blocks,
+    _prepacked_block_sparse_gemm_2d_compact_from_active_blocks,
+    _prepacked_block_sparse_gemm_2d_from_active_blocks,
+    _scatter_compact_to_dense_output,
+)
 
 
 def __getattr__(name: str):
