@@ -47,7 +47,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="down_sweep", choices=["down_sweep", "llama", "fused", "decode", "perstep"])
+    ap.add_argument("--workload", default="down_sweep",
+                    choices=["down_sweep", "llama", "fused", "decode", "perstep", "2d"])
     ap.add_argument("--batches", default=None, help="perstep workload: batch sizes (default: all six)")
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
@@ -329,6 +330,80 @@ def _graph_time(fns, reps, warmup=2):
         b.synchronize()
         ts.append(a.elapsed_time(b) * 1000.0)
     return statistics.median(ts), statistics.mean(ts)
+
+
+def run_2d(args, dev):
+    """2-D block sparsity (SURVEY rank-4 "next" row): down_proj B=16 with half of the K-blocks
+    active and a sweep of active 64-column output blocks, in place and compact.  Each point is
+    a graph of launches rotated over >= 1 GiB of weight copies; parity against the oracle
+    first.  Bytes per launch: na * 64 * (nn * 64) * 2 (active weight)."""
+    import numpy as np
+    import torch
+
+    import bsa_mi355x as bsa
+    from bsa_mi355x import sparse2d
+    from oracle import bsg_oracle as orc
+
+    bt, k, n = 16, 11008, 4096
+    nb_k, nb_n = orc.nblk_of(k), n // 64
+    x, w_kn, kidx = orc.make_inputs(1234, bt, k, n, "laplace", na=orc.n_active_for_sparsity(0.5, nb_k))
+    rng = np.random.default_rng(4321)
+    xt, kt = torch.from_numpy(x).to(dev), torch.from_numpy(kidx).to(dev)
+    packed0 = bsa.pack_weight(torch.from_numpy(w_kn).to(dev), layout="kn")
+    copies = max(1, math.ceil(ROTATE_BYTES / packed0.numel() / 2))
+    packed = [packed0] + [packed0.clone() for _ in range(copies - 1)]
+    w_nk = np.ascontiguousarray(w_kn.T)
+    reps = max(5, args.steps)
+    rows, total_bytes, total_us, focus = [], 0, 0.0, None
+    for nd, compact in ((1.0, False), (0.75, False), (0.5, False), (0.25, False), (0.5, True)):
+        nn = int(round(nd * nb_n))
+        nidx = np.sort(rng.choice(nb_n, nn, replace=False)).astype(np.int32)
+        nt = torch.from_numpy(nidx).to(dev)
+        y = torch.zeros(bt, nn * 64 if compact else n, dtype=torch.float16, device=dev)
+        pl = sparse2d.plan_2d(bt, n, nn, nb_k, len(kidx), dev)
+
+        def call(i, nt=nt, y=y, compact=compact, pl=pl):
+            return lambda: sparse2d.gemm_2d_packed(xt, packed[i % copies], n, kt, nt, y, compact=compact, plan=pl,
+                                                   workspace_prefix="bench2d")
+
+        call(0)()
+        torch.cuda.synchronize()
+        want = orc.gemm_2d_ref(x, w_nk, kidx, nidx, out_init=np.zeros((bt, n), np.float32), compact=compact)
+        if not orc.within_tolerance(y.float().cpu().numpy(), want):
+            raise SystemExit(f"2-D parity failure at n-density {nd} compact={compact}")
+        med, mean = _graph_time([call(i) for i in range(copies)], reps)
+        us, us_mean = med / copies, mean / copies
+        b = len(kidx) * 64 * nn * 64 * 2
+        total_bytes += b * copies
+        total_us += med
+        name = f"down_b16_k500_n{int(round(nd * 1000)):04d}{'_compact' if compact else ''}"
+        row = {"name": name, "active_k_blocks": len(kidx), "active_n_blocks": nn, "compact": compact,
+               "us_per_gemm": round(us, 3), "GBps_active": round(b / (us * 1e-6) / 1e9, 1), "plan": list(pl.as_tuple())}
+        rows.append(row)
+        log(json.dumps(row))
+        if nd == 0.5 and not compact:
+            focus = (row, b, us_mean)
+    full = rows[0]["us_per_gemm"]
+    for r in rows[1:]:
+        r["speedup_vs_all_n_blocks"] = round(full / r["us_per_gemm"], 3)
+        r["ideal"] = round(nb_n / r["active_n_blocks"], 3)
+    frow, fb, fmean = focus
+    achieved = fb / (fmean * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(total_bytes / (total_us * 1e-6) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps, "warmup": 2, "ms_per_step": round(total_us / 1000.0, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: numpy PCG64 seed 1234 (X~Laplace(0,0.05), W~N(0,0.02)), K mask rng.choice of 86/172, "
+                "output-block masks rng.choice seed 4321; weights rotated over >=1 GiB of copies",
+        "config": {"workload": "2-D block sparsity: down_proj B=16 K=11008 N=4096, K density 0.5, output-block "
+                               "density {1, 0.75, 0.5, 0.25} in place + 0.5 compact"},
+        "points": rows,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "bsg_gemm_kernel (2-D)",
+                     "point": frow["name"], "avg_launch_us": round(fmean, 3), "bytes_per_launch": fb},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
 
 
 def run_fused(args, dev):
@@ -626,6 +701,9 @@ def main():
         return
     elif args.workload == "perstep":
         run_perstep(args, dev)
+        return
+    elif args.workload == "2d":
+        run_2d(args, dev)
         return
     else:
         run_decode(args, dev)

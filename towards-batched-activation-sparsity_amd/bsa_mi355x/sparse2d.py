@@ -18,8 +18,8 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from ._lib import Plan, check, load
-from .runtime import (BLOCK_K, MAX_NBLK, _dtype_code, _pad_k, _packed_entry, _require_cuda, _sort_active_blocks_asc,
-                      _stream_handle, _workspace, ctypes_byref, resolve_plan)
+from .runtime import (BLOCK_K, MAX_NBLK, _cu_count, _dtype_code, _pad_k, _packed_entry, _require_cuda,
+                      _sort_active_blocks_asc, _stream_handle, _workspace, ctypes_byref, resolve_plan)
 
 INDEX_BLOCK_OUT_META_SIZE = 64  # output-block width of the 2-D path (KRN:19)
 BLOCK_N_OUT = INDEX_BLOCK_OUT_META_SIZE
@@ -48,20 +48,29 @@ def _int32_dev(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
 
 def plan_2d(bt: int, n_dim: int, nn: int, nblk: int, na: int, device: torch.device, plan: Optional[Plan] = None,
             dense: bool = False) -> Plan:
-    """A plan whose work-group covers at most one 64-column output block.  The tuned table is
-    looked up for the active width (nn * 64 columns); a tuned plan wider than 64 columns
-    falls back to the library's heuristics, an explicit one raises."""
-    pl = resolve_plan(bt, max(nn, 1) * BLOCK_N_OUT, nblk, na, device, plan, dense=dense)
-    if pl.group_cols() <= BLOCK_N_OUT:
-        return pl
-    if plan is not None and any(plan.as_tuple()):
-        raise ValueError(f"2-D sparsity needs a plan covering at most {BLOCK_N_OUT} columns per work-group; "
-                         f"{pl.as_tuple()} covers {pl.group_cols()}")
-    pl = resolve_plan(bt, max(nn, 1) * BLOCK_N_OUT, nblk, na, device, None, dense=dense, lookup_plan=False)
+    """A plan whose work-group covers at most one 64-column output block.  An explicit plan is
+    kept (and rejected when wider).  Otherwise the tile is the one the 1-D path uses for the
+    full N (the tuned table), or the library's when that one is wider than 64 columns, and the
+    split-K factor fills the chip without a partial second round: floor(CUs / work-groups),
+    at most 4 for 32- and 64-row tiles (their partials are large) and 8 otherwise, measured on
+    down_proj B=16 and B=64 with 16-64 of 64 output blocks."""
+    explicit = plan is not None and any(plan.as_tuple())
+    pl = resolve_plan(bt, n_dim, nblk, na, device, plan, dense=dense)
     if pl.group_cols() > BLOCK_N_OUT:
-        pl = resolve_plan(bt, max(nn, 1) * BLOCK_N_OUT, nblk, na, device,
-                          Plan(pl.split_k, 16, 0, 0, pl.rows_per_group, pl.kind), dense=dense, lookup_plan=False)
-    return pl
+        if explicit:
+            raise ValueError(f"2-D sparsity needs a plan covering at most {BLOCK_N_OUT} columns per work-group; "
+                             f"{pl.as_tuple()} covers {pl.group_cols()}")
+        pl = resolve_plan(bt, n_dim, nblk, na, device, Plan(1, 16, 0, 0, pl.rows_per_group, pl.kind), dense=dense,
+                          lookup_plan=False)
+    if explicit and plan.split_k:
+        return pl
+    groups = max(1, nn) * (BLOCK_N_OUT // pl.group_cols()) * (-(-int(bt) // pl.rows_per_group))
+    cap = 4 if pl.rows_per_group >= 32 else 8
+    splitters = pl.waves_per_group if pl.kind == 1 else 1
+    sk = max(1, min(cap, _cu_count(device) // groups, max(1, int(na) // (2 * splitters))))
+    if pl.kind == 3:
+        sk = 1
+    return Plan(sk, pl.cols_per_wave, pl.waves_per_group, pl.depth, pl.rows_per_group, pl.kind)
 
 
 def gemm_2d_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_blocks: Optional[torch.Tensor],
