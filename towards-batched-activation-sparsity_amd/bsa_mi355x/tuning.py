@@ -218,6 +218,16 @@ class _Case:
         return statistics.median(ts)
 
 
+def _time_or_inf(case: "_Case", plan: Plan, dense: bool = False) -> float:
+    """A candidate the library rejects for this case (BsgUnsupported) never wins."""
+    from ._lib import BsgUnsupported
+
+    try:
+        return case.time(plan, dense=dense)
+    except BsgUnsupported:
+        return float("inf")
+
+
 def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densities: Sequence[float],
          out_table: str = TABLE_PATH, lookup_dir: Optional[str] = None, rotate_bytes: int = 1 << 30,
          seed: int = 1234, log=print, merge_from: Optional[str] = None) -> List[dict]:
@@ -236,7 +246,7 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
             case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes)
             dense_best = (float("inf"), None)
             for p in candidate_plans(bt, nblk, nblk):
-                us = case.time(p, dense=True)
+                us = _time_or_inf(case, p, dense=True)
                 if us < dense_best[0]:
                     dense_best = (us, p)
             entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": nblk, "dense": True,
@@ -247,7 +257,7 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
                 case.idx = torch.randperm(nblk, generator=gen)[:na].sort()[0].to(torch.int32).to(dev)
                 best = (float("inf"), None)
                 for p in candidate_plans(bt, na, nblk):
-                    us = case.time(p)
+                    us = _time_or_inf(case, p)
                     if us < best[0]:
                         best = (us, p)
                 entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": na, "dense": False,
