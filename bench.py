@@ -333,7 +333,7 @@ def _graph_time(fns, reps, warmup=2):
 
 
 def run_2d(args, dev):
-    """2-D block sparsity (SURVEY rank-4 "next" row): down_proj B=16 with half of the K-blocks
+    """2-D block sparsity (active output blocks as well as K-blocks): down_proj B=16 with half of the K-blocks
     active and a sweep of active 64-column output blocks, in place and compact.  Each point is
     a graph of launches rotated over >= 1 GiB of weight copies; parity against the oracle
     first.  Bytes per launch: na * 64 * (nn * 64) * 2 (active weight)."""
@@ -554,7 +554,7 @@ class ShapePool:
 
 
 def run_perstep(args, dev):
-    """Oracle-map replay (the reference's headline,
+    """Oracle-map replay (the reference's headline benchmark,
     scripts/bench_perstep_actual_kernel_speedup.py): for each batch size, every group-step's
     S-map of 7 projections x 32 layers (tests/golden/perstep_smaps.npz, from the reference's
     results/oracle/perstep_batch_sweep.json) gives 224 GEMMs with density 1 - S and

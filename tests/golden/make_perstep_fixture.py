@@ -1,7 +1,7 @@
 """Write tests/golden/perstep_smaps.npz from the reference's committed result files (data only):
 
 - results/oracle/perstep_batch_sweep.json: the per-step oracle sparsity maps S[7 projections]
-  [32 layers] for B in {2,4,8,16,32,64} x 5 groups x 11 decode steps (SURVEY RES_O), on a
+  [32 layers] for B in {2,4,8,16,32,64} x 5 groups x 11 decode steps, on a
   0.1 grid, stored here as uint8 tenths, with each group-step's mean sparsity;
 - results/kernel/perstep_actual_kernel_speedup.json: the reference's published A100X kernel
   speedups over cuBLAS dense for those maps (per batch size and per group-step).

@@ -7,14 +7,21 @@ gfx950 only; Python reaches it through ctypes (bsa_mi355x/_lib.py).
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_ROOT = os.path.dirname(os.path.abspath(__file__))
 REPO_ROOT = os.path.dirname(PKG_ROOT)
-SRC = os.path.join(PKG_ROOT, "csrc", "bsgemm.hip")
+CSRC = os.path.join(PKG_ROOT, "csrc")
+# The C ABI and host code, then the tile tables (each instantiates a slice of the kernel
+# templates of bsg_device.hpp); the units compile in parallel and link into one library.
+SOURCES = ["bsgemm.hip", "tiles_k1_r16.hip", "tiles_k1_r32.hip", "tiles_k1_r64.hip", "tiles_k2.hip",
+           "tiles_k4.hip", "tiles_k3.hip"]
+SRC = os.path.join(CSRC, "bsgemm.hip")
 INCLUDE = os.path.join(REPO_ROOT, "include")
 OUT = os.path.join(PKG_ROOT, "bsa_mi355x", "libbsgemm.so")
 
@@ -23,11 +30,11 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-mcode-object-version=5",
-    # Packed-FP32 VALU forms are kept out of every kernel (build notes).
+    # Packed-FP32 VALU forms (v_pk_*_f32) are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -37,19 +44,30 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libbsgemm.so)")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile libbsgemm.so (always recompiles) and return its path."""
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, SRC, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (proc.stderr or "").splitlines() if noise not in l)
+    err = "\n".join(l for l in (proc.stderr or "").splitlines() if NOISE not in l)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd[-3:])}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile libbsgemm.so (always recompiles every unit) and return its path."""
+    cc = hipcc()
+    jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with tempfile.TemporaryDirectory(prefix="bsgemm_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[cc, *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, s), "-o", o]
+                for s, o in zip(SOURCES, objs)]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        tmp = OUT + ".tmp"
+        _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
     os.replace(tmp, OUT)
     return OUT
 

@@ -1,5 +1,8 @@
-// bsgemm.hip — gfx950 (MI355X / CDNA4) kernels and C ABI for the batch-shared
-// 64-channel block-sparse GEMM  Y[bt,N] = sum_{j active} X[bt,64j:64j+64] · W[64j:64j+64,N].
+// bsgemm.hip — gfx950 (MI355X / CDNA4) C ABI, plan resolution, launches and the selector,
+// packing and helper kernels for the batch-shared 64-channel block-sparse GEMM
+//   Y[bt,N] = sum_{j active} X[bt,64j:64j+64] · W[64j:64j+64,N].
+// The GEMM kernel templates are in bsg_device.hpp; their instantiated tiles are split over
+// tiles_*.hip (one table per translation unit, compiled in parallel).
 //
 // Reference semantics: kernels/shared_mask_batched_triton_min_runtime.py
 //   naive list kernel 684-733, bitmap kernel 814-874, split-K write/reduce 1898-1988,
@@ -30,6 +33,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "bsg_device.hpp"
 #include "bsgemm.h"
 
 #define BSG_VERSION_STR "bsgemm 0.1 (gfx950, mfma_f32_16x16x32)"
@@ -49,897 +53,6 @@ int fail(int code, const char* fmt, ...) {
 int hip_fail(hipError_t e, const char* what) {
   return fail(BSG_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr int kOOB = (int)0x80000000u;  // buffer offset beyond any num_records we build
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
-
-enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2, MODE_TOPK = 3 };
-// A GEMM ranks block scores itself (MODE_TOPK) up to this many blocks: keys and ranks fit its
-// block-list buffer, and a one-wave work-group flags at most 8 per thread.
-#define BSG_TOPK_MAX_NBLK 512
-
-// Kind 3 activation staging: 1 KiB loads per wave, and the LDS it may take.
-#define BSG_FMA_X_LOADS 16
-#define BSG_FMA_LDS_MAX (96 * 1024)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_bytes, kRsrcWord3);
-}
-
-__device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int voff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
-}
-
-#ifndef BSG_W_AUX
-#define BSG_W_AUX 2  // weight stream: non-temporal (read once, keep X resident in L1/L2)
-#endif
-
-__device__ __forceinline__ u32x4 ld16_stream(__amdgpu_buffer_rsrc_t r, int voff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, BSG_W_AUX);
-}
-
-template <typename T>
-struct Elem;
-
-template <>
-struct Elem<_Float16> {
-  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t bits(float f) {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
-  }
-  // a.lo*b.lo + a.hi*b.hi + c: fp16 products are exact in fp32, one fp32 rounding per add.
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
-  }
-};
-
-template <>
-struct Elem<__bf16> {
-  static __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t bits(float f) {
-    return __builtin_bit_cast(uint16_t, (__bf16)f);
-  }
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-  }
-};
-
-// Exclusive prefix sum over the work-group; also returns the total.  `scratch` holds
-// one int per wave.  Contains two barriers.
-template <int NT>
-__device__ __forceinline__ int wg_exclusive_scan(int v, int* scratch, int* total) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int o = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += o;
-  }
-  if (lane == 63) scratch[w] = incl;
-  __syncthreads();
-  int base = 0, tot = 0;
-#pragma unroll
-  for (int i = 0; i < NT / 64; ++i) {
-    int s = scratch[i];
-    if (i < w) base += s;
-    tot += s;
-  }
-  __syncthreads();
-  *total = tot;
-  return base + incl - v;
-}
-
-// The one-work-group top-k (1024 threads) flags at most 2 blocks per thread (kept flags: one
-// 32-bit mask per thread).
-static_assert(BSG_MAX_NBLK <= 32 * 1024, "selector chunk layout");
-
-// Rank of block j among nb scores in LDS, ordered (score desc, block id asc): the number of
-// blocks ahead of it.  s_sc holds the nb scores followed by zeros up to a multiple of 16 (a pad
-// is never ahead: its score is the lowest and its id >= nb).  The scores are read as LDS
-// broadcasts into two 8-score buffers, each refilled while the other is compared, so the loop
-// runs at the compare rate rather than the LDS round trip.  UNIQUE: the scores are distinct keys
-// that already encode the id order, so one compare does.  Rolled on purpose: a work-group runs
-// it once, so unrolled copies cost more in cold instruction fetch than they save.
-template <bool UNIQUE, typename S>
-__device__ __forceinline__ int rank_of(const S* s_sc, int nb, int j, S sj) {
-  const int nb16 = (nb + 15) & ~15;
-  int rank = 0;
-  S a[8], b[8];
-  auto count = [&](const S (&v)[8], int i0) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if constexpr (UNIQUE)
-        rank += v[u] > sj;
-      else
-        rank += (v[u] > sj) | ((v[u] == sj) & (i0 + u < j));
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < 8; ++u) a[u] = s_sc[u];
-#pragma unroll 1
-  for (int i0 = 0; i0 < nb16; i0 += 16) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) b[u] = s_sc[i0 + 8 + u];
-    __builtin_amdgcn_sched_barrier(0);
-    count(a, i0);
-    const int in = i0 + 16 < nb16 ? i0 + 16 : 0;  // the last refill is a harmless re-read
-#pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = s_sc[in + u];
-    __builtin_amdgcn_sched_barrier(0);
-    count(b, i0 + 8);
-  }
-  return rank;
-}
-
-// Zero the pad of a score array after its nb entries, up to a multiple of 16 (rank_of).
-template <typename S>
-__device__ __forceinline__ void pad_scores(S* s_sc, int nb) {
-  const int tid = threadIdx.x;
-  if (tid < ((nb + 15) & ~15) - nb) s_sc[nb + tid] = S(0);
-}
-
-// Top-k of nb exact-L1 block scores (global memory, written by an earlier kernel on the
-// stream): ranked (score desc, id asc), the first k kept, their ids handed to emit(position,
-// id) in ascending id order.  keyed: every score is below 2^53, so (score << 11) | (2047 - id)
-// is a unique key in the same order and one compare decides.  The nb^2 compares are spread over
-// every wave of the work-group: a work item is (64 blocks, 16 scores), each lane counts the
-// scores ahead of its block and adds the count to the block's rank in LDS.  s_key holds nb
-// keys rounded up to 16, s_rank nb ints; each thread then flags a contiguous chunk of at most
-// 32 blocks (nb <= 32 * NT), so a scan of the counts gives ascending positions.  Returns
-// min(k, nb).  Every thread has finished reading s_key and s_rank when emit runs (the scan's
-// barriers lie between), so emit may overwrite them.
-template <int NT, typename Emit>
-__device__ __forceinline__ int topk_l1_list(const uint64_t* scores, int nb, int k, bool keyed, uint64_t* s_key,
-                                            int* s_rank, int* s_scan, Emit emit) {
-  constexpr int W = NT / 64;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb16 = (nb + 15) & ~15;
-  for (int i = tid; i < nb16; i += NT) {
-    uint64_t key = 0;  // pads: lowest score, ids >= nb, never ahead
-    if (i < nb) {
-      const uint64_t v = scores[i];
-      key = keyed ? (v << 11) | (uint64_t)(BSG_MAX_NBLK - 1 - i) : v;
-    }
-    s_key[i] = key;
-  }
-  for (int i = tid; i < nb; i += NT) s_rank[i] = 0;
-  __syncthreads();
-  const int C = nb16 / 16;
-  const int items = ((nb + 63) / 64) * C;
-#pragma unroll 1
-  for (int it = w; it < items; it += W) {
-    const int g = it / C;
-    const int i0 = 16 * (it - g * C);
-    const int j = 64 * g + lane;
-    const uint64_t kj = j < nb ? s_key[j] : 0;
-    uint64_t ki[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) ki[u] = s_key[i0 + u];
-    int r = 0;
-    if (keyed) {
-#pragma unroll
-      for (int u = 0; u < 16; ++u) r += ki[u] > kj;
-    } else {
-#pragma unroll
-      for (int u = 0; u < 16; ++u) r += (ki[u] > kj) | ((ki[u] == kj) & (i0 + u < j));
-    }
-    if (j < nb && r != 0) atomicAdd(&s_rank[j], r);
-  }
-  __syncthreads();
-  const int per = (nb + NT - 1) / NT;
-  const int beg = tid * per < nb ? tid * per : nb;
-  const int end = beg + per < nb ? beg + per : nb;
-  const int kk = k < nb ? k : nb;
-  uint32_t selmask = 0;
-  int c = 0;
-#pragma unroll 1
-  for (int q = 0; q < end - beg; ++q)
-    if (s_rank[beg + q] < kk) {
-      selmask |= 1u << q;
-      ++c;
-    }
-  int total = 0;
-  int o = wg_exclusive_scan<NT>(c, s_scan, &total);
-#pragma unroll 1
-  for (int q = 0; q < end - beg; ++q)
-    if ((selmask >> q) & 1u) emit(o++, beg + q);
-  return kk;
-}
-
-
-// Split-K hand-off primitives.  Partials move with agent-scope relaxed atomics, which are
-// device-coherent without touching the rest of L2 (an agent-scope fence would write back and
-// invalidate the whole L2 of the XCD on every work-group).
-
-__device__ __forceinline__ void part_store(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Components of one fragment lane sit 64 floats apart (see the partial layout).
-__device__ __forceinline__ f32x4 part_load(const float* q) {
-  f32x4 v;
-  v.x = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.y = __hip_atomic_load(q + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.z = __hip_atomic_load(q + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v.w = __hip_atomic_load(q + 192, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
-}
-
-// Every store of this wave has completed (at the scope it was issued with).
-__device__ __forceinline__ void part_publish() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt(7), lgkmcnt(15)
-}
-
-__device__ __forceinline__ unsigned counter_add(uint32_t* c) {
-  return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void counter_reset(uint32_t* c) {
-  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-struct GemmParams {
-  const void* x;
-  const void* wp;
-  void* y;
-  const int32_t* idx;
-  const int32_t* na_dev;
-  const uint8_t* bitmap;
-  float* part;
-  uint32_t* cnt;
-  int64_t ldx;
-  int64_t ldy;
-  int32_t bt, K, N, npad, nblk, nbm, na, mode, split_k, n_tiles, x_bytes, y_fast;
-  // MODE_TOPK: exact-L1 block scores (na = k), whether they fit the unique-key order, and where
-  // work-group (0, 0) publishes the kept list and its count (null: not published)
-  const uint64_t* scores;
-  int32_t* idx_out;
-  int32_t* na_out;
-  int32_t keyed;
-  // 2-D sparsity: ascending active 64-column output blocks (null: every column), their count
-  // (host value, or the device one when nn_dev is set), whether Y is compact (active blocks
-  // side by side), and the width Y stores are bounded by (N, or nn * 64 when compact)
-  const int32_t* nidx;
-  const int32_t* nn_dev;
-  int32_t nn, ncompact, ny;
-};
-
-// ---------------------------------------------------------------------------------------
-// Pieces shared by both GEMM kernel kinds.
-
-// Work-group -> (column tile, split) with an XCD-aware order: hardware places work-group b
-// on XCD b % 8, so consecutive logical ids (the split partners of a tile) share an XCD.
-__device__ __forceinline__ void tile_of_group(int split_k, int* tile, int* sk) {
-  const int nwg = gridDim.x;
-  const int bid = blockIdx.x;
-  const int lid = (nwg & 7) == 0 ? (bid & 7) * (nwg >> 3) + (bid >> 3) : bid;
-  *tile = lid / split_k;
-  *sk = lid - *tile * split_k;
-}
-
-// Columns of column tile `tile` (gc columns wide): n0 = first weight column it reads, n0y =
-// first output column it writes.  N2D (2-D sparsity, a separate instantiation so the 1-D
-// kernels carry none of it): tile t is piece t % (64/gc) of active 64-column block
-// nidx[t / (64/gc)]; compact output packs the active blocks side by side.  Returns false when
-// the tile has no block (past the device-side count): the whole work-group then returns
-// before any barrier.  A block id outside [0, ceil(N/64)) reads past the packed columns (zero
-// weights) and writes nothing.
-template <bool N2D>
-__device__ __forceinline__ bool tile_columns(const GemmParams& p, int tile, int gc, int* n0, int* n0y) {
-  if constexpr (!N2D) {
-    *n0 = *n0y = tile * gc;
-    return true;
-  }
-  const int per = 64 / gc;
-  const int bi = tile / per;
-  int nn = p.nn;
-  if (p.nn_dev != nullptr) {
-    const int d = __builtin_amdgcn_readfirstlane(*p.nn_dev);
-    nn = d < 0 ? 0 : (d < nn ? d : nn);
-  }
-  if (bi >= nn) return false;
-  const int off = (tile - bi * per) * gc;
-  const int nb = __builtin_amdgcn_readfirstlane(p.nidx[bi]);
-  const bool ok = nb >= 0 && nb < (p.N + 63) / 64;
-  *n0 = ok ? nb * 64 + off : p.npad;
-  *n0y = p.ncompact ? bi * 64 + off : (ok ? *n0 : p.ny);
-  return true;
-}
-
-// Stage this call's active-block list in LDS (list copy, bitmap compaction, top-k of block
-// scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
-// and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
-// second (up to 512 blocks).
-template <int NT>
-__device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
-  const int tid = threadIdx.x;
-  int na;
-  if (p.mode == MODE_TOPK) {
-    // Every work-group ranks the scores itself (identically), so the list needs no other
-    // launch; keys and ranks are staged in the list buffer and overwritten by the kept ids.
-    na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
-                          s_scan, [&](int pos, int id) { s_ids[pos] = id; });
-  } else if (p.mode == MODE_LIST) {
-    na = p.na;
-    if (p.na_dev != nullptr) {
-      const int d = *p.na_dev;
-      na = d < 0 ? 0 : (d < na ? d : na);
-    }
-    for (int i = tid; i < na; i += NT) s_ids[i] = p.idx[i];
-  } else if (p.mode == MODE_BITMAP) {
-    const int per = (p.nbm + NT - 1) / NT;
-    const int beg = tid * per < p.nbm ? tid * per : p.nbm;
-    const int end = beg + per < p.nbm ? beg + per : p.nbm;
-    int c = 0;
-    for (int i = beg; i < end; ++i) c += p.bitmap[i] != 0;
-    int total = 0;
-    int o = wg_exclusive_scan<NT>(c, s_scan, &total);
-    for (int i = beg; i < end; ++i)
-      if (p.bitmap[i] != 0) s_ids[o++] = i;
-    na = total;
-  } else {
-    na = p.nblk;
-    for (int i = tid; i < na; i += NT) s_ids[i] = i;
-  }
-  na = __builtin_amdgcn_readfirstlane(na);
-  __syncthreads();
-  if (p.mode == MODE_TOPK && p.idx_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
-    for (int i = tid; i < na; i += NT) p.idx_out[i] = s_ids[i];
-    if (tid == 0) *p.na_out = na;
-  }
-  return na;
-}
-
-// Output fragment g = bi * CS + cs of a work-group whose columns start at n0 (CS 16-column
-// subtiles): lane holds Y[y0 + 16 bi + lane%16][n0 + 16 cs + 4 (lane/16) + r], r = 0..3.
-template <typename T, int CS>
-__device__ __forceinline__ void store_y(const GemmParams& p, int y0, int n0, int g, f32x4 v) {
-  const int lane = threadIdx.x & 63;
-  const int bi = g / CS;
-  const int cs = g - bi * CS;
-  const int b = y0 + 16 * bi + (lane & 15);
-  const int n = n0 + 16 * cs + 4 * (lane >> 4);
-  if (b >= p.bt) return;
-  uint16_t* yrow = (uint16_t*)p.y + (size_t)b * (size_t)p.ldy;
-  if (p.y_fast) {
-    if (n < p.ny) {
-      u32x2 pk;
-      pk.x = (uint32_t)Elem<T>::bits(v.x) | ((uint32_t)Elem<T>::bits(v.y) << 16);
-      pk.y = (uint32_t)Elem<T>::bits(v.z) | ((uint32_t)Elem<T>::bits(v.w) << 16);
-      *(u32x2*)(yrow + n) = pk;
-    }
-  } else {
-    if (n + 0 < p.ny) yrow[n + 0] = Elem<T>::bits(v.x);
-    if (n + 1 < p.ny) yrow[n + 1] = Elem<T>::bits(v.y);
-    if (n + 2 < p.ny) yrow[n + 2] = Elem<T>::bits(v.z);
-    if (n + 3 < p.ny) yrow[n + 3] = Elem<T>::bits(v.w);
-  }
-}
-
-// Partials: [tile][split][fragment][component][lane] floats, so every dword store or load
-// instruction of a wave covers 256 contiguous bytes.
-template <int FT>
-__device__ __forceinline__ void part_emit(const GemmParams& p, size_t tile_lin, int sk, int g, f32x4 v) {
-  float* dst = (float*)p.part + ((tile_lin * p.split_k + sk) * FT + g) * 256 + (threadIdx.x & 63);
-  part_store(dst + 0, v.x);
-  part_store(dst + 64, v.y);
-  part_store(dst + 128, v.z);
-  part_store(dst + 192, v.w);
-}
-
-// Split-K hand-off: publish this work-group's partials, count arrivals; the last work-group
-// of the tile reduces the FT fragments in split order and re-arms the counter for the next
-// launch (graph-replay safe).  Partials move through agent-scope (device-coherent) stores and
-// loads, so no L2 write-back/invalidate is needed: each wave waits for its own stores, the
-// barrier orders them before the counter update, and the last work-group loads only after it
-// has seen the final count.
-template <typename T, int FT, int CS, int WPG>
-__device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_lin, int y0, int n0, int w,
-                                              int* s_flag) {
-  const int S = p.split_k;
-  const int lane = threadIdx.x & 63;
-  part_publish();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = counter_add(&p.cnt[tile_lin]);
-    *s_flag = prev == (unsigned)(S - 1);
-  }
-  __syncthreads();
-  if (!*s_flag) return;
-  // Work items (fragment, split) of this wave are requested 16 at a time before any is
-  // consumed (one memory round trip per 16), then summed per fragment in split order.
-  const float* base = (const float*)p.part + (tile_lin * S) * FT * 256 + lane;
-  constexpr int FW = (FT + WPG - 1) / WPG;  // fragments per wave
-  f32x4 acc2[FW];
-#pragma unroll
-  for (int i = 0; i < FW; ++i) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int items = FW * S;
-  for (int i0 = 0; i0 < items; i0 += 16) {
-    f32x4 t[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int it = i0 + i;
-      const int fi = it / S, q = it - fi * S, g = w + fi * WPG;
-      if (it < items && g < FT) t[i] = part_load(base + ((size_t)q * FT + g) * 256);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int it = i0 + i;
-      const int fi = it / S, g = w + fi * WPG;
-      if (it < items && g < FT) {
-#pragma unroll
-        for (int j = 0; j < FW; ++j)
-          if (j == fi) acc2[j] += t[i];
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < FW; ++j)
-    if (w + j * WPG < FT) store_y<T, CS>(p, y0, n0, w + j * WPG, acc2[j]);
-  if (threadIdx.x == 0) counter_reset(&p.cnt[tile_lin]);
-}
-
-// ---------------------------------------------------------------------------------------
-// Kind 1 ("ksplit"): one work-group = BTT*16 batch rows x NSUB*16 columns; its WPG waves split
-// the work-group's share of the block list into contiguous slices and are reduced through LDS
-// in wave order.  Each wave loads its own X fragments.  Best when bt is small (the X fragments
-// are few) and many narrow column tiles are needed to fill the chip.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D>
-__global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
-  constexpr int NT = 64 * WPG;
-  constexpr int F = BTT * NSUB;
-  constexpr int RED_BYTES = WPG > 1 ? (WPG - 1) * F * 64 * 16 : 0;  // waves 1..WPG-1
-  constexpr int IDS_BYTES = BSG_MAX_NBLK * 4;
-  // The block list (main loop) and the wave-reduction buffer (epilogue) share LDS.
-  __shared__ __attribute__((aligned(16))) char s_mem[RED_BYTES > IDS_BYTES ? RED_BYTES : IDS_BYTES];
-  __shared__ int s_misc[WPG + 2];
-  int* const s_ids = (int*)s_mem;
-  f32x4* const s_red = (f32x4*)s_mem;
-
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int tile, sk;
-  tile_of_group(p.split_k, &tile, &sk);
-  const int S = p.split_k;
-  int n0, n0y;
-  if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
-  const int y0 = blockIdx.y * (16 * BTT);
-
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
-
-  // This wave's contiguous slice [pbeg, pend) of the list.
-  const int G = S * WPG;
-  const int g = sk * WPG + w;
-  const int pbeg = (int)(((int64_t)na * g) / G);
-  const int pend = (int)(((int64_t)na * (g + 1)) / G);
-  const int cnt = pend - pbeg;
-
-  const int blk_bytes = p.npad * 128;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
-  int xrow_off[BTT];
-  bool xrow_ok[BTT];
-#pragma unroll
-  for (int bi = 0; bi < BTT; ++bi) {
-    const int row = y0 + 16 * bi + (lane & 15);
-    xrow_ok[bi] = row < p.bt;
-    xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
-  }
-  const int xcol = 8 * (lane >> 4);
-  const int wcol = lane * 16 + (n0 >> 4) * 2048;
-
-  u32x4 wv[DEPTH][NSUB][2];
-  u32x4 xv[DEPTH][BTT][2];
-  f32x4 acc[BTT][NSUB];
-#pragma unroll
-  for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto issue = [&](u32x4 (&wd)[NSUB][2], u32x4 (&xd)[BTT][2], int t) {
-    const int q = t < cnt ? pbeg + t : 0;
-    int blk = s_ids[q];
-    blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
-    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
-      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
-    }
-    const int kb = (ok ? blk : 0) * 64 + xcol;
-#pragma unroll
-    for (int bi = 0; bi < BTT; ++bi) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int col = kb + 32 * h;
-        const bool v = ok && xrow_ok[bi] && col < p.K;
-        xd[bi][h] = ld16(xr, v ? xrow_off[bi] + col * 2 : kOOB);
-      }
-    }
-  };
-
-  auto compute = [&](const u32x4 (&wd)[NSUB][2], const u32x4 (&xd)[BTT][2]) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][h], xd[bi][h], acc[bi][s]);
-  };
-
-  // Rolling pipeline: DEPTH blocks in flight; loads past the slice are out-of-range (zero,
-  // no memory traffic) so the body has no data-dependent branches.
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
-  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      compute(wv[d], xv[d]);
-      issue(wv[d], xv[d], t0 + d + DEPTH);
-    }
-  }
-
-  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
-  auto emit = [&](int f, f32x4 v) {
-    if (S == 1)
-      store_y<T, NSUB>(p, y0, n0y, f, v);
-    else
-      part_emit<F>(p, tile_lin, sk, f, v);
-  };
-
-  if constexpr (WPG > 1) {
-    // Waves 1..WPG-1 hand their accumulators to wave 0 through LDS; wave 0 sums in wave
-    // order and emits every fragment.
-    __syncthreads();  // every wave is done reading s_ids before s_red overwrites it
-    if (w > 0) {
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) s_red[((w - 1) * F + bi * NSUB + s) * 64 + lane] = acc[bi][s];
-    }
-    __syncthreads();
-    if (w == 0) {
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) {
-          f32x4 v = acc[bi][s];
-          for (int ww = 1; ww < WPG; ++ww) v += s_red[((ww - 1) * F + bi * NSUB + s) * 64 + lane];
-          emit(bi * NSUB + s, v);
-        }
-    }
-  } else {
-#pragma unroll
-    for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-      for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
-  }
-
-  if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
-}
-
-// Kinds 2 and 4 ("xlds"): one work-group = BTT*16 batch rows x WC*NSUB*16 columns; its waves
-// walk the same block list together.  Each block's X tile (BTT*16 rows x 64 channels) is loaded
-// once per work-group, in MFMA B-fragment order, into a double-buffered LDS stage (one barrier
-// per block) and shared by every wave, so X costs 1/WPG of the loads of kind 1 and the prefetch
-// registers hold weights only.  Kind 2 (WK = 1): the WC waves split the columns.  Kind 4
-// (WK = 2): 2*WC waves, column group x 32-channel half of every block, so each wave issues half
-// the MFMAs and LDS reads of a block and two waves share each SIMD, overlapping one wave's
-// barrier and LDS waits with the other's MFMAs; the halves are summed through LDS at the end.
-template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D>
-__global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p) {
-  constexpr int WPG = WC * WK;
-  constexpr int NT = 64 * WPG;
-  constexpr int XF = 2 * BTT;                // X fragments (1 KiB each) per block
-  constexpr int XPW = (XF + WPG - 1) / WPG;  // X fragments each wave loads per block
-  constexpr int CS = WC * NSUB;              // 16-column subtiles per work-group
-  constexpr int FT = BTT * CS;               // output fragments per work-group
-  constexpr int HPW = 2 / WK;                // channel halves per wave
-  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
-  __shared__ __attribute__((aligned(16))) u32x4 s_x[2][XF][64];
-  __shared__ __attribute__((aligned(16))) f32x4 s_red[WK > 1 ? WC * BTT * NSUB : 1][64];
-  __shared__ int s_misc[WPG + 2];
-
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wc = w % WC;  // column group
-  const int wk = w / WC;  // channel half (kind 4)
-  int tile, sk;
-  tile_of_group(p.split_k, &tile, &sk);
-  const int S = p.split_k;
-  int n0, n0y;
-  if (!tile_columns<N2D>(p, tile, 16 * CS, &n0, &n0y)) return;
-  const int y0 = blockIdx.y * (16 * BTT);
-
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
-
-  // The work-group's contiguous slice of the list (all its waves walk it together).
-  const int pbeg = (int)(((int64_t)na * sk) / S);
-  const int pend = (int)(((int64_t)na * (sk + 1)) / S);
-  const int cnt = pend - pbeg;
-
-  const int blk_bytes = p.npad * 128;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
-  // X fragments this wave brings in: f = w + j*WPG -> batch tile f/2, k-half f%2.
-  int xrow_off[XPW];
-  bool xrow_ok[XPW];
-  int xcol[XPW];
-#pragma unroll
-  for (int j = 0; j < XPW; ++j) {
-    const int f = w + j * WPG;
-    const int row = y0 + 16 * (f >> 1) + (lane & 15);
-    xrow_ok[j] = f < XF && row < p.bt;
-    xrow_off[j] = xrow_ok[j] ? row * (int)p.ldx * 2 : 0;
-    xcol[j] = 32 * (f & 1) + 8 * (lane >> 4);
-  }
-  const int wcol = lane * 16 + ((n0 >> 4) + wc * NSUB) * 2048;
-
-  u32x4 wv[DEPTH][NSUB][HPW];
-  u32x4 xs[DEPTH][XPW];
-  f32x4 acc[BTT][NSUB];
-#pragma unroll
-  for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto issue = [&](u32x4 (&wd)[NSUB][HPW], u32x4 (&xd)[XPW], int t) {
-    const int q = t < cnt ? pbeg + t : 0;
-    int blk = s_ids[q];
-    blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
-    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-      for (int hh = 0; hh < HPW; ++hh) wd[s][hh] = ld16_stream(wr, wcol + s * 2048 + (WK > 1 ? wk : hh) * 1024);
-    const int kb = (ok ? blk : 0) * 64;
-#pragma unroll
-    for (int j = 0; j < XPW; ++j) {
-      const int col = kb + xcol[j];
-      const bool v = ok && xrow_ok[j] && col < p.K;
-      xd[j] = ld16(xr, v ? xrow_off[j] + col * 2 : kOOB);
-    }
-  };
-
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xs[d], d);
-  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int stage = (t0 + d) & 1;
-      // Publish X of block t0+d; after the barrier every wave has also finished reading the
-      // stage it will overwrite next iteration.
-#pragma unroll
-      for (int j = 0; j < XPW; ++j)
-        if (w + j * WPG < XF) s_x[stage][w + j * WPG][lane] = xs[d][j];
-      __syncthreads();
-#pragma unroll
-      for (int hh = 0; hh < HPW; ++hh) {
-        const int h = WK > 1 ? wk : hh;
-#pragma unroll
-        for (int bi = 0; bi < BTT; ++bi) {
-          const u32x4 xb = s_x[stage][2 * bi + h][lane];
-#pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xb, acc[bi][s]);
-        }
-      }
-      issue(wv[d], xs[d], t0 + d + DEPTH);
-    }
-  }
-
-  if constexpr (WK > 1) {
-    // The second channel half hands its accumulators to the first through LDS.
-    if (wk == 1) {
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) s_red[(wc * BTT + bi) * NSUB + s][lane] = acc[bi][s];
-    }
-    __syncthreads();
-    if (wk == 0) {
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) acc[bi][s] += s_red[(wc * BTT + bi) * NSUB + s][lane];
-    }
-  }
-
-  const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
-  if (wk == 0) {
-#pragma unroll
-    for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-      for (int s = 0; s < NSUB; ++s) {
-        const int g = bi * CS + wc * NSUB + s;
-        if (S == 1)
-          store_y<T, CS>(p, y0, n0y, g, acc[bi][s]);
-        else
-          part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
-      }
-  }
-  if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
-}
-
-// Kind 3 ("fma", batch tiles of 1-8 rows): the contraction is too thin for MFMA, so each lane
-// multiplies the 8 consecutive channels of one weight column that its 16-byte load of the packed
-// tile holds (channels 32h + 8g .. +7 of column c, g = lane / 16, c = lane % 16) with the same
-// channels of every batch row, in fp32 with packed fp16/bf16 dot products, and the four lanes
-// of a column (g = 0..3) are summed once at the end.  The work-group's activations (its whole
-// block list, BT rows x 64 channels per block) are staged in LDS once at the start, in
-// [block][row][half h][group g] 16-byte order, so each of those reads is a broadcast; the loop
-// then streams weights only.  The waves split the work-group's block list (as kind 1) and are
-// reduced through LDS in wave order.
-template <typename T, int BT, int NSUB, int WPG, int DEPTH, bool N2D>
-__global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
-  constexpr int NT = 64 * WPG;
-  constexpr int XI = BSG_FMA_X_LOADS;  // staging loads per wave (host guarantees enough)
-  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
-  __shared__ float s_red[WPG > 1 ? WPG - 1 : 1][NSUB * BT][16];
-  __shared__ int s_misc[WPG + 2];
-  extern __shared__ __attribute__((aligned(16))) u32x4 s_xs[];  // [na][BT][2][4]
-
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x;
-  int n0, n0y;
-  if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
-  const int y0 = blockIdx.y * BT;
-
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
-  const int pbeg = (int)(((int64_t)na * w) / WPG);
-  const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
-  const int cnt = pend - pbeg;
-
-  // Stage X: 16-byte piece e = (q*BT + b)*8 + (4h + g) of the list holds x[y0+b][64 ids[q] + 32h + 8g ..];
-  // wave w loads pieces (i*WPG + w)*64 + lane, i < nxi.
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
-  const int pieces = na * BT * 8;
-  const int nxi = (pieces + NT - 1) / NT;
-  int qid[XI];  // block id of each staged piece, read as one batch
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int q = ((i * WPG + w) * 64 + lane) / (BT * 8);
-    qid[i] = s_ids[q < na ? q : 0];
-  }
-  const int blk_bytes = p.npad * 128;
-  const int wcol = lane * 16 + (n0 >> 4) * 2048;
-  u32x4 wv[DEPTH][NSUB][2];
-  float acc[NSUB][BT];
-#pragma unroll
-  for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-    for (int b = 0; b < BT; ++b) acc[s][b] = 0.f;
-
-  auto issue = [&](u32x4 (&wd)[NSUB][2], int t) {
-    const int qq = t < cnt ? pbeg + t : 0;
-    int blk = s_ids[qq];
-    blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
-    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      wd[s][0] = ld16_stream(wr, wcol + s * 2048);
-      wd[s][1] = ld16_stream(wr, wcol + s * 2048 + 1024);
-    }
-  };
-
-  // The first weight loads go out ahead of the staging loads: the first block needs both.
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
-  u32x4 xs[XI];
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    if (i < nxi) {
-      const int e = (i * WPG + w) * 64 + lane;
-      const int blk = e < pieces ? qid[i] : -1;
-      const int row = y0 + (e / 8) % BT;
-      const int col = blk * 64 + (e & 7) * 8;
-      const bool v = blk >= 0 && blk < p.nblk && row < p.bt && col < p.K;
-      xs[i] = ld16(xr, v ? row * (int)p.ldx * 2 + col * 2 : kOOB);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < XI; ++i) {
-    const int e = (i * WPG + w) * 64 + lane;
-    if (i < nxi && e < pieces) s_xs[e] = xs[i];
-  }
-  __syncthreads();
-
-  // The X pieces of a block are read from LDS XD blocks ahead of its dot products (LDS latency
-  // off the per-block path); XD shrinks as the batch tile grows to bound the registers.
-  constexpr int XD = BT >= 8 ? 1 : (BT >= 4 ? 2 : DEPTH);
-  static_assert(DEPTH % XD == 0, "X prefetch distance");
-  const int g = lane >> 4;
-  u32x4 xv[XD][2][BT];
-  auto xread = [&](u32x4 (&xd)[2][BT], int t) {
-    // Positions past the slice carry zero weights; read a valid X piece for them.
-    const int q = pbeg + (t < cnt ? t : cnt - 1);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int b = 0; b < BT; ++b) xd[h][b] = s_xs[((q * BT + b) * 2 + h) * 4 + g];
-  };
-  auto compute = [&](const u32x4 (&wd)[NSUB][2], const u32x4 (&xd)[2][BT]) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int b = 0; b < BT; ++b)
-#pragma unroll
-        for (int s = 0; s < NSUB; ++s) {
-          float a = acc[s][b];
-          a = Elem<T>::dot2(wd[s][h].x, xd[h][b].x, a);
-          a = Elem<T>::dot2(wd[s][h].y, xd[h][b].y, a);
-          a = Elem<T>::dot2(wd[s][h].z, xd[h][b].z, a);
-          acc[s][b] = Elem<T>::dot2(wd[s][h].w, xd[h][b].w, a);
-        }
-  };
-
-  if (cnt > 0) {
-#pragma unroll
-    for (int k = 0; k < XD; ++k) xread(xv[k], k);
-    for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        compute(wv[d], xv[d % XD]);
-        xread(xv[d % XD], t0 + d + XD);
-        issue(wv[d], t0 + d + DEPTH);
-      }
-    }
-  }
-
-  // Column c of subtile s: the lanes c, c+16, c+32, c+48 hold its four channel groups.
-#pragma unroll
-  for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-    for (int b = 0; b < BT; ++b) {
-      float v = acc[s][b];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      acc[s][b] = v;
-    }
-  if constexpr (WPG > 1) {
-    if (w > 0 && lane < 16) {
-#pragma unroll
-      for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-        for (int b = 0; b < BT; ++b) s_red[w - 1][s * BT + b][lane] = acc[s][b];
-    }
-    __syncthreads();
-  }
-  if (w == 0 && lane < 16) {
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      const int n = n0y + 16 * s + lane;
-#pragma unroll
-      for (int b = 0; b < BT; ++b) {
-        float v = acc[s][b];
-        for (int ww = 1; ww < WPG; ++ww) v += s_red[ww - 1][s * BT + b][lane];
-        const int row = y0 + b;
-        if (row < p.bt && n < p.ny) ((uint16_t*)p.y)[(size_t)row * (size_t)p.ldy + n] = Elem<T>::bits(v);
-      }
-    }
-  }
-}
-
 
 // Reference scoring rules (scripts/bench_roundrobin_e2e_decode.py:90-176) on the device, in
 // fp64: per block j over its 64 channels, with b over the bt rows,
@@ -1288,95 +401,15 @@ __global__ __launch_bounds__(1024) void bsg_nmask_kernel(const uint8_t* __restri
   if (tid == 0) *count = base;
 }
 
-typedef void (*GemmFn)(GemmParams);
-
-enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4 };
-
-// 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
-struct KernelEntry {
-  int kind, rows, nsub, wpg, depth;
-  GemmFn f16, bf16, f16_2d, bf16_2d;
-};
-
-// The 2-D instantiation of a tile, or null when its work-group covers more than one 64-column
-// output block (the discarded branch is never instantiated).
-template <int KIND, typename T, int B, int S, int W, int D>
-constexpr GemmFn kernel_2d() {
-  constexpr int gc = KIND == KIND_XLDS ? 16 * S * W : (KIND == KIND_XLDS_KH ? 16 * S * (W / 2) : 16 * S);
-  if constexpr (gc > 64) {
-    return nullptr;
-  } else if constexpr (KIND == KIND_KSPLIT) {
-    return bsg_gemm_kernel<T, B, S, W, D, true>;
-  } else if constexpr (KIND == KIND_XLDS) {
-    return bsg_gemm_xl_kernel<T, B, S, W, 1, D, true>;
-  } else if constexpr (KIND == KIND_XLDS_KH) {
-    return bsg_gemm_xl_kernel<T, B, S, W / 2, 2, D, true>;
-  } else {
-    return bsg_gemm_fma_kernel<T, B, S, W, D, true>;
-  }
-}
-
-#define BSG_K(B, S, W, D)                                                                                          \
-  {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D, false>, bsg_gemm_kernel<__bf16, B, S, W, D, false>, \
-   kernel_2d<KIND_KSPLIT, _Float16, B, S, W, D>(), kernel_2d<KIND_KSPLIT, __bf16, B, S, W, D>()}
-#define BSG_X(B, S, W, D)                                                                     \
-  {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false>,           \
-   bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D, false>, kernel_2d<KIND_XLDS, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>()}
-#define BSG_Y(B, S, W, D)                                                                        \
-  {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false>,        \
-   bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D, false>, kernel_2d<KIND_XLDS_KH, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>()}
-#define BSG_F(R, S, W, D)                                                                                 \
-  {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
-   kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>()}
-
-// Instantiated tile set.  Kind 1 registers per lane ~ depth*(nsub+btt)*8 + btt*nsub*4;
-// kind 2 ~ depth*(nsub*8 + ceil(2*btt/wpg)*4) + btt*nsub*4.
-const KernelEntry kKernels[] = {
-    // kind 1, 16 batch rows
-    BSG_K(1, 1, 1, 4), BSG_K(1, 1, 1, 8), BSG_K(1, 1, 2, 4), BSG_K(1, 1, 2, 8),
-    BSG_K(1, 1, 4, 2), BSG_K(1, 1, 4, 4), BSG_K(1, 1, 4, 8), BSG_K(1, 1, 8, 2),
-    BSG_K(1, 1, 8, 4), BSG_K(1, 1, 8, 8),
-    BSG_K(1, 2, 1, 4), BSG_K(1, 2, 1, 8), BSG_K(1, 2, 2, 4), BSG_K(1, 2, 2, 8),
-    BSG_K(1, 2, 4, 2), BSG_K(1, 2, 4, 4), BSG_K(1, 2, 4, 8), BSG_K(1, 2, 8, 2),
-    BSG_K(1, 2, 8, 4),
-    BSG_K(1, 4, 1, 4), BSG_K(1, 4, 2, 4), BSG_K(1, 4, 4, 2), BSG_K(1, 4, 4, 4),
-    BSG_K(1, 4, 8, 2),
-    BSG_K(1, 8, 1, 2), BSG_K(1, 8, 2, 2), BSG_K(1, 8, 4, 2),
-    // kind 1, 32 batch rows
-    BSG_K(2, 2, 1, 4), BSG_K(2, 2, 2, 4), BSG_K(2, 2, 4, 2), BSG_K(2, 2, 4, 4),
-    BSG_K(2, 4, 1, 4), BSG_K(2, 4, 2, 2), BSG_K(2, 4, 2, 4), BSG_K(2, 4, 4, 2),
-    // kind 1, 64 batch rows
-    BSG_K(4, 2, 1, 4), BSG_K(4, 2, 2, 2), BSG_K(4, 2, 2, 4), BSG_K(4, 2, 4, 2),
-    BSG_K(4, 4, 1, 2), BSG_K(4, 4, 1, 4), BSG_K(4, 4, 2, 2), BSG_K(4, 4, 4, 1),
-    BSG_K(4, 4, 4, 2),
-    BSG_K(4, 8, 1, 2), BSG_K(4, 8, 2, 1), BSG_K(4, 8, 2, 2),
-    // kind 2 (X staged in LDS, waves split columns)
-    BSG_X(1, 1, 2, 4), BSG_X(1, 1, 4, 4), BSG_X(1, 1, 4, 8), BSG_X(1, 1, 8, 4), BSG_X(1, 2, 2, 4),
-    BSG_X(1, 2, 4, 4),
-    BSG_X(2, 1, 2, 4), BSG_X(2, 1, 4, 4), BSG_X(2, 1, 4, 8), BSG_X(2, 2, 2, 4), BSG_X(2, 2, 4, 4),
-    BSG_X(4, 1, 2, 4), BSG_X(4, 1, 4, 4), BSG_X(4, 1, 4, 8), BSG_X(4, 1, 8, 4), BSG_X(4, 2, 2, 2),
-    BSG_X(4, 2, 2, 4), BSG_X(4, 2, 4, 2), BSG_X(4, 2, 4, 4), BSG_X(4, 4, 2, 2), BSG_X(4, 4, 4, 2),
-    // kind 4 (as kind 2, waves also split the two channel halves of every block)
-    BSG_Y(4, 1, 8, 4), BSG_Y(4, 1, 8, 2), BSG_Y(4, 1, 8, 8), BSG_Y(4, 2, 8, 2), BSG_Y(4, 2, 8, 4),
-    BSG_Y(4, 1, 4, 4), BSG_Y(4, 2, 4, 4), BSG_Y(4, 1, 4, 8),
-    BSG_Y(2, 1, 8, 4), BSG_Y(2, 1, 4, 4), BSG_Y(2, 2, 4, 4),
-    BSG_Y(1, 1, 8, 4), BSG_Y(1, 1, 4, 4),
-    // kind 3 (fp32 dot products, 1-8 batch rows, X staged in LDS)
-    BSG_F(1, 1, 2, 4), BSG_F(1, 1, 4, 4), BSG_F(1, 1, 4, 8), BSG_F(1, 1, 8, 4), BSG_F(1, 2, 4, 4),
-    BSG_F(2, 1, 2, 4), BSG_F(2, 1, 4, 4), BSG_F(2, 1, 4, 8), BSG_F(2, 1, 8, 4), BSG_F(2, 2, 4, 4),
-    BSG_F(4, 1, 2, 4), BSG_F(4, 1, 4, 4), BSG_F(4, 1, 4, 8), BSG_F(4, 1, 8, 4), BSG_F(4, 2, 4, 4),
-    BSG_F(8, 1, 2, 4), BSG_F(8, 1, 4, 4), BSG_F(8, 1, 4, 8), BSG_F(8, 1, 8, 4), BSG_F(8, 2, 4, 4),
-};
-#undef BSG_K
-#undef BSG_X
-#undef BSG_F
-#undef BSG_Y
+// The whole instantiated tile set, one table per translation unit.
+const TileTable* const kTables[] = {&kTilesK1R16, &kTilesK1R32, &kTilesK1R64, &kTilesK2, &kTilesK4, &kTilesK3};
 
 const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
-  for (const KernelEntry& e : kKernels)
-    if (e.kind == kind && e.rows == rows && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
+  for (const TileTable* t : kTables)
+    for (int i = 0; i < t->n; ++i) {
+      const KernelEntry& e = t->e[i];
+      if (e.kind == kind && e.rows == rows && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
+    }
   return nullptr;
 }
 
@@ -1462,18 +495,20 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
     // that keeps every explicit field and is closest in the automatic ones.
     const KernelEntry* best = nullptr;
     int best_d = 1 << 30;
-    for (const KernelEntry& e : kKernels) {
-      if (e.kind != pl->kind || e.rows != rpg) continue;
-      if (!(auto_fields & 1) && e.nsub * 16 != pl->cols_per_wave) continue;
-      if (!(auto_fields & 2) && e.wpg != pl->waves_per_group) continue;
-      if (!(auto_fields & 4) && e.depth != pl->depth) continue;
-      const int d = abs(e.nsub * 16 - pl->cols_per_wave) * 64 + abs(e.wpg - pl->waves_per_group) * 8 +
-                    abs(e.depth - pl->depth);
-      if (d < best_d) {
-        best_d = d;
-        best = &e;
+    for (const TileTable* t : kTables)
+      for (int i = 0; i < t->n; ++i) {
+        const KernelEntry& e = t->e[i];
+        if (e.kind != pl->kind || e.rows != rpg) continue;
+        if (!(auto_fields & 1) && e.nsub * 16 != pl->cols_per_wave) continue;
+        if (!(auto_fields & 2) && e.wpg != pl->waves_per_group) continue;
+        if (!(auto_fields & 4) && e.depth != pl->depth) continue;
+        const int d = abs(e.nsub * 16 - pl->cols_per_wave) * 64 + abs(e.wpg - pl->waves_per_group) * 8 +
+                      abs(e.depth - pl->depth);
+        if (d < best_d) {
+          best_d = d;
+          best = &e;
+        }
       }
-    }
     if (best) {
       pl->cols_per_wave = best->nsub * 16;
       pl->waves_per_group = best->wpg;
