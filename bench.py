@@ -35,7 +35,11 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 1 << 30
 METRIC = "µs/GEMM + HBM GB/s + speedup vs dense, Llama-2-7B shapes at B=2/16/64"
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md")
+# Committed PMC summaries (HBM bytes per launch) of the roofline point of each workload.
+TRAFFIC_PROFILES = {
+    "down_b16_s500": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md"),
+    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_xl_gate_up_b64_s520.md"),
+}
 
 
 def log(msg: str) -> None:
@@ -216,11 +220,14 @@ def cpu_baseline(point, seconds):
     }
 
 
-def load_traffic():
-    """HBM bytes per launch of the roofline point, from the committed PMC summary (a line
-    `traffic_bytes_per_launch: <int>`), or None when no summary is present."""
+def load_traffic(point):
+    """HBM bytes per launch of a roofline point, from its committed PMC summary (a line
+    `traffic_bytes_per_launch: <int>`), or None when that point has no summary."""
+    path = TRAFFIC_PROFILES.get(point)
+    if path is None:
+        return None
     try:
-        with open(PROFILE_TRAFFIC) as f:
+        with open(path) as f:
             for line in f:
                 if line.strip().startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1].strip())
@@ -760,7 +767,7 @@ def main():
     f_med, f_mean = per[focus]
     achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(focus),
                 "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
                 "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes}
     if not args.only:
