@@ -99,3 +99,21 @@ def test_cpu_tensors_are_rejected():
     out = torch.zeros(2, 1, 16, dtype=torch.float16)
     with pytest.raises(ValueError):
         bsa._prepacked_block_sparse_gemm_from_active_blocks(x, w, torch.tensor([0], dtype=torch.int32), out)
+
+
+def test_bench_traffic_profile_per_roofline_point():
+    """Each workload's roofline point reads the PMC summary of that same point, and the figure
+    is at least the point's algorithmic bytes (active weight na*64*N*2)."""
+    import importlib.util
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    algorithmic = {"down_b16_s500": 86 * 64 * 4096 * 2, "gate_up_b64_s520": 31 * 64 * 11008 * 2}
+    assert set(bench.TRAFFIC_PROFILES) == set(algorithmic)
+    for point, path in bench.TRAFFIC_PROFILES.items():
+        assert point.split("_s")[0].replace("_", "") in os.path.basename(path).replace("_", "")
+        t = bench.load_traffic(point)
+        assert isinstance(t, int) and algorithmic[point] <= t < 1.2 * algorithmic[point], (point, t)
+    assert bench.load_traffic("qkvo_b2_s803") is None
