@@ -165,3 +165,49 @@ def test_2d_rejects_a_wide_plan(dev):
     x, w_nk, kb = case(65, bt, kdim, n, 10, "normal")
     with pytest.raises(ValueError):
         _run(dev, x, w_nk, kb, [1], False, plan=(1, 32, 4, 4, 32, 2))  # 128 columns per work-group
+
+
+def test_every_2d_tile(dev):
+    """Every tile with a 2-D instantiation (work-group columns dividing 64): fp16 in place and
+    compact, and bf16 in place, over output blocks that include the partial last one.  Columns
+    outside the listed blocks keep the sentinel bit for bit."""
+    bt, kdim, n = 37, 4096, 1000  # 16 output blocks, the last 40 columns wide; 3 row groups of 16
+    x, w_nk, kb = case(66, bt, kdim, n, 29, "normal")
+    nb = [0, 3, 15]
+    xb = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    wb = torch.from_numpy(w_nk.astype(np.float32)).to(torch.bfloat16)
+    init = np.full((bt, n), SENTINEL, dtype=np.float32)
+    ref = {c: orc.gemm_2d_ref(x, w_nk, kb, nb, out_init=init, compact=c) for c in (False, True)}
+    ref_b = orc.gemm_2d_ref(xb.float().numpy(), wb.float().numpy(), kb, nb, out_init=init)
+    written = np.zeros(n, bool)
+    for b in nb:
+        written[64 * b:min(64 * b + 64, n)] = True
+    packed, packed_b = bsa.pack_weight(to_dev(w_nk, dev)), bsa.pack_weight(wb.to(dev))
+    xt, xbt = to_dev(x, dev), xb.to(dev)
+    kbt, nbt = to_dev(kb, dev), to_dev(np.asarray(nb, np.int32), dev)
+    tiles = [t for t in bsa.kernel_tiles()
+             if 64 % bsa.Plan(1, t[2], t[3], t[4], t[1], t[0]).group_cols() == 0]
+    assert len(tiles) >= 50
+    for kind, rows, cols, waves, depth in tiles:
+        p = bsa.Plan(1 if kind == 3 else 2, cols, waves, depth, rows, kind)
+        what = f"2d tile kind={kind} rows={rows} cols={cols} waves={waves} depth={depth}"
+        print(what, flush=True)
+        for compact in (False, True):
+            y = torch.full((bt, 64 * len(nb) if compact else n), SENTINEL, dtype=torch.float16, device=dev)
+            s2d.gemm_2d_packed(xt, packed, n, kbt, nbt, y, compact=compact, plan=p)
+            torch.cuda.synchronize()
+            yv = y.float().cpu().numpy()
+            if compact:
+                assert_close(yv, ref[True], f"{what} compact")
+            else:
+                assert np.all(yv[:, ~written] == SENTINEL), f"{what}: columns outside the blocks were written"
+                assert_close(yv[:, written], ref[False][:, written], what)
+        yb = torch.full((bt, n), SENTINEL, dtype=torch.bfloat16, device=dev)
+        s2d.gemm_2d_packed(xbt, packed_b, n, kbt, nbt, yb, plan=p)
+        torch.cuda.synchronize()
+        ybv = yb.float().cpu().numpy()
+        assert np.all(ybv[:, ~written] == SENTINEL), f"{what} bf16: columns outside the blocks were written"
+        # bf16 output keeps 8 significant bits: tolerance 5e-3 rel. Frobenius, 2e-2 max-abs
+        got, want = ybv[:, written], ref_b[:, written]
+        rf = orc.rel_frobenius(got, want)
+        assert rf <= 5e-3 and np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want)), f"{what} bf16: {rf:.3e}"
