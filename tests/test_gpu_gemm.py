@@ -261,3 +261,37 @@ def test_down_proj_sparsity_sweep(dev, s):
     else:
         y = _run_list(dev, x, w_nk, idx, prefix="sweep")
     assert_close(y, orc.gemm_ref(x, w_nk, idx), f"down s={s}")
+
+
+@pytest.mark.parametrize("plan", [
+    (3, 16, 1, 4, 16, 1), (3, 16, 2, 4, 16, 1), (3, 16, 4, 4, 16, 1), (3, 16, 8, 4, 16, 1),  # kind 1, 64-512 threads
+    (3, 32, 2, 4, 32, 1),
+    (3, 16, 4, 4, 16, 2), (3, 16, 2, 4, 32, 2), (3, 16, 8, 4, 64, 2),  # kind 2
+    (3, 16, 8, 4, 64, 4), (3, 16, 4, 4, 32, 4),                        # kind 4
+    (1, 16, 4, 4, 2, 3), (1, 16, 8, 4, 2, 3),                          # kind 3
+])
+def test_block_sources_every_work_group_size(dev, plan):
+    """Bitmap (compacted by a work-group scan whose width is the kernel's thread count), list
+    with a device-side count, and dense, for every kernel kind and work-group size, split-K 3
+    where the kind has it; bt=37 spans several row groups."""
+    bt, k, n = 37, 11008, 1000
+    nb = orc.nblk_of(k)
+    x, w_nk, _ = case(17, bt, k, n, 1)
+    rng = np.random.default_rng(plan[2] * 100 + plan[5])
+    bm = (rng.random(nb) < 0.6).astype(np.uint8)
+    lst = rng.permutation(nb)[:120].astype(np.int32)
+    p = bsa.Plan(*plan)
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    out = torch.empty(bt, n, dtype=F16, device=dev)
+    bsa.gemm_packed(xt, packed, n, None, out, bitmap=to_dev(bm, dev), plan=p, workspace_prefix="srcs")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.flatnonzero(bm)), f"bitmap {plan}")
+    cnt = torch.tensor([77], dtype=torch.int32, device=dev)
+    bsa.gemm_packed(xt, packed, n, to_dev(lst, dev), out, num_active=120, num_active_dev=cnt, plan=p,
+                    workspace_prefix="srcs")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, lst[:77]), f"device count {plan}")
+    bsa.gemm_packed(xt, packed, n, None, out, plan=p, workspace_prefix="srcs")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.arange(nb)), f"dense {plan}")
