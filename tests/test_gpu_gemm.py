@@ -295,3 +295,31 @@ def test_block_sources_every_work_group_size(dev, plan):
     bsa.gemm_packed(xt, packed, n, None, out, plan=p, workspace_prefix="srcs")
     torch.cuda.synchronize()
     assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.arange(nb)), f"dense {plan}")
+
+
+def test_maximum_block_count(dev):
+    """K = 64 * 2048, the most K-blocks the kernels take (BSG_MAX_NBLK): every block as a
+    permuted list, as a bitmap and dense; the exact-L1 selector ranks all 2048 blocks."""
+    bt, k, n = 3, 64 * 2048, 48
+    nb = orc.nblk_of(k)
+    assert nb == 2048
+    x, w_nk, _ = case(18, bt, k, n, 1)
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    out = torch.empty(bt, n, dtype=F16, device=dev)
+    want = orc.gemm_ref64(x, w_nk, np.arange(nb))
+    perm = np.random.default_rng(5).permutation(nb).astype(np.int32)
+    bsa.gemm_packed(xt, packed, n, to_dev(perm, dev), out, workspace_prefix="maxblk")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), want, "2048-block list")
+    bsa.gemm_packed(xt, packed, n, None, out, bitmap=torch.ones(nb, dtype=torch.uint8, device=dev),
+                    workspace_prefix="maxblk")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), want, "2048-block bitmap")
+    bsa.gemm_packed(xt, packed, n, None, out, workspace_prefix="maxblk")
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), want, "2048-block dense")
+    idx, cnt = bsa.select_topk_l1(xt, 1000, workspace_prefix="maxblk_sel")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 1000
+    assert np.array_equal(idx.cpu().numpy()[:1000], orc.select_topk_l1(x, 1000))
