@@ -323,3 +323,24 @@ def test_maximum_block_count(dev):
     torch.cuda.synchronize()
     assert int(cnt.item()) == 1000
     assert np.array_equal(idx.cpu().numpy()[:1000], orc.select_topk_l1(x, 1000))
+
+
+@pytest.mark.parametrize("plan", [(1, 16, 2, 4, 16, 1), (3, 16, 4, 4, 32, 2), (2, 16, 8, 4, 64, 4), (1, 16, 4, 4, 4, 3)])
+def test_strided_rows_and_side_stream(dev, plan):
+    """X and Y as row-strided views (ldx > K, ldy > N), launched on a side stream: the padding
+    columns of X hold NaN (any read past K would poison Y) and those of Y keep a sentinel."""
+    bt, k, n, na = 40, 4096, 1000, 25
+    x, w_nk, idx = case(19, bt, k, n, na)
+    x_wide = torch.full((bt, k + 64), float("nan"), dtype=F16, device=dev)
+    x_wide[:, :k] = to_dev(x, dev)
+    y_wide = torch.full((bt, n + 24), 7.0, dtype=F16, device=dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    it = to_dev(idx, dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        bsa.gemm_packed(x_wide[:, :k], packed, n, it, y_wide[:, :n], plan=bsa.Plan(*plan), workspace_prefix="strided")
+    s.synchronize()
+    y = y_wide.float().cpu().numpy()
+    assert np.all(y[:, n:] == 7.0), "columns past N were written"
+    assert_close(y[:, :n], orc.gemm_ref64(x, w_nk, idx), f"strided {plan}")
