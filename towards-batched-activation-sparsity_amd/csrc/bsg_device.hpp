@@ -889,6 +889,10 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
         compute(wv[d], xv[d % XD]);
         xread(xv[d % XD], t0 + d + XD);
         issue(wv[d], t0 + d + DEPTH);
+        // Keep block d's loads between its dot products and block d+1's: left free, the
+        // scheduler gathers every dot product of the pass above every load, so each pass
+        // starts by waiting for all DEPTH blocks in flight and the pipeline drains.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
