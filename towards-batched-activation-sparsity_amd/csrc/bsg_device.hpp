@@ -829,9 +829,9 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     }
   };
 
-  // The first weight loads go out ahead of the staging loads: the first block needs both.
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
+  // The staging loads go out first and the first weight loads right behind them: loads complete
+  // in issue order, so waiting for the staging then leaves the weight loads in flight across
+  // the LDS writes and the barrier instead of draining the pipeline before the loop starts.
   u32x4 xs[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
@@ -844,6 +844,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
       xs[i] = ld16(xr, v ? row * (int)p.ldx * 2 + col * 2 : kOOB);
     }
   }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int e = (i * WPG + w) * 64 + lane;
