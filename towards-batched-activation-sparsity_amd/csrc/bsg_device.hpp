@@ -769,11 +769,12 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
 // multiplies the 8 consecutive channels of one weight column that its 16-byte load of the packed
 // tile holds (channels 32h + 8g .. +7 of column c, g = lane / 16, c = lane % 16) with the same
 // channels of every batch row, in fp32 with packed fp16/bf16 dot products, and the four lanes
-// of a column (g = 0..3) are summed once at the end.  The work-group's activations (its whole
-// block list, BT rows x 64 channels per block) are staged in LDS once at the start, in
-// [block][row][half h][group g] 16-byte order, so each of those reads is a broadcast; the loop
-// then streams weights only.  The waves split the work-group's block list (as kind 1) and are
-// reduced through LDS in wave order.
+// of a column (g = 0..3) are summed once at the end.  The waves split the work-group's block
+// list (as kind 1); each wave stages the activations of its own slice (BT rows x 64 channels per
+// block) in LDS once at the start, in [list position][row][half h][group g] 16-byte order, so
+// each of its later reads is a broadcast and the loop streams weights only.  A wave reads only
+// what it wrote, and one wave's LDS accesses complete in order, so the staging needs no
+// barrier.  The waves are reduced through LDS in wave order.
 template <typename T, int BT, int NSUB, int WPG, int DEPTH, bool N2D>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
@@ -795,16 +796,18 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
   const int cnt = pend - pbeg;
 
-  // Stage X: 16-byte piece e = (q*BT + b)*8 + (4h + g) of the list holds x[y0+b][64 ids[q] + 32h + 8g ..];
-  // wave w loads pieces (i*WPG + w)*64 + lane, i < nxi.
+  // Stage this wave's slice of X: 16-byte piece e = (q*BT + b)*8 + (4h + g) holds
+  // x[y0+b][64 ids[q] + 32h + 8g ..] for list positions q in [pbeg, pend); the wave loads its
+  // pieces pbeg*BT*8 + i*64 + lane, i < nxi.
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
-  const int pieces = na * BT * 8;
-  const int nxi = (pieces + NT - 1) / NT;
+  const int e0 = pbeg * BT * 8;
+  const int pieces = cnt * BT * 8;
+  const int nxi = (pieces + 63) / 64;
   int qid[XI];  // block id of each staged piece, read as one batch
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
-    const int q = ((i * WPG + w) * 64 + lane) / (BT * 8);
-    qid[i] = s_ids[q < na ? q : 0];
+    const int q = pbeg + (i * 64 + lane) / (BT * 8);
+    qid[i] = s_ids[q < pend ? q : 0];
   }
   const int blk_bytes = p.npad * 128;
   const int wcol = lane * 16 + (n0 >> 4) * 2048;
@@ -830,13 +833,12 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   };
 
   // The staging loads go out first and the first weight loads right behind them: loads complete
-  // in issue order, so waiting for the staging then leaves the weight loads in flight across
-  // the LDS writes and the barrier instead of draining the pipeline before the loop starts.
+  // in issue order, so waiting for the staging leaves the weight loads in flight.
   u32x4 xs[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     if (i < nxi) {
-      const int e = (i * WPG + w) * 64 + lane;
+      const int e = i * 64 + lane;
       const int blk = e < pieces ? qid[i] : -1;
       const int row = y0 + (e / 8) % BT;
       const int col = blk * 64 + (e & 7) * 8;
@@ -848,10 +850,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
-    const int e = (i * WPG + w) * 64 + lane;
-    if (i < nxi && e < pieces) s_xs[e] = xs[i];
+    const int e = i * 64 + lane;
+    if (i < nxi && e < pieces) s_xs[e0 + e] = xs[i];
   }
-  __syncthreads();
+  // The wave's staging writes have completed before any of its reads of them is issued.
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
 
   // The X pieces of a block are read from LDS XD blocks ahead of its dot products (LDS latency
   // off the per-block path); XD shrinks as the batch tile grows to bound the registers.

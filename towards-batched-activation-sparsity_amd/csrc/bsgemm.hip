@@ -413,10 +413,11 @@ const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth)
   return nullptr;
 }
 
-// Kind 3 stages the work-group's whole list of activation blocks in LDS with at most
-// BSG_FMA_X_LOADS 1 KiB loads per wave: na * rows pieces of 128 B.
+// Kind 3: each wave stages its slice of the list's activation blocks (at most ceil(na / wpg)
+// blocks x rows pieces of 128 B) in LDS with at most BSG_FMA_X_LOADS 1 KiB loads, and the
+// work-group's list takes na x rows x 128 B of LDS.
 bool fma_fits(int64_t na, int rows, int wpg) {
-  return na * rows <= (int64_t)BSG_FMA_X_LOADS * 8 * wpg && na * rows * 128 <= BSG_FMA_LDS_MAX;
+  return (na + wpg - 1) / wpg * rows <= (int64_t)BSG_FMA_X_LOADS * 8 && na * rows * 128 <= BSG_FMA_LDS_MAX;
 }
 
 int pow2_ceil(int64_t v) {
