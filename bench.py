@@ -623,6 +623,7 @@ def run_perstep(args, dev):
             total_bytes += na * 64 * p.n * 2
             total_us += us
         step_own, step_mm = [], []
+        dense_total = sparse_total = 0.0
         for m in maps:
             d_sum = m_sum = s_sum = 0.0
             for pi in range(7):
@@ -634,6 +635,13 @@ def run_perstep(args, dev):
                     m_sum += mm_us[name]
             step_own.append(d_sum / s_sum)
             step_mm.append(m_sum / s_sum)
+            dense_total += d_sum
+            sparse_total += s_sum
+        # Kernel replay throughput as scripts/analyze_perstep_kernel_replay_throughput.py:22-44 defines
+        # it: batch tokens (B x group-steps) over the summed step kernel times (not end-to-end tokens/s)
+        tokens = bt * len(sel)
+        ref_dense_ms = float(np.sum(fx["ref_step_dense_ms"][sel]))
+        ref_sparse_ms = float(np.sum(fx["ref_step_sparse_ms"][sel]))
         ref_i = list(fx["ref_batch"]).index(bt) if bt in list(fx["ref_batch"]) else None
         row = {"B": bt, "group_steps": int(len(sel)), "mean_sparsity": round(float(fx["mean_sparsity"][sel].mean()), 4),
                "unique_cases": len(cases),
@@ -644,7 +652,13 @@ def run_perstep(args, dev):
                "dense_us": {k: round(v, 2) for k, v in dense_us.items()},
                "hipblaslt_us": {k: round(v, 2) for k, v in mm_us.items()},
                "sparse_us_step_mean": round(float(np.mean([sum(sparse_us[(PERSTEP_PROJ_SHAPE[pi], 10 - int(t))][0]
-                                                               for pi in range(7) for t in m[pi]) for m in maps])), 1)}
+                                                               for pi in range(7) for t in m[pi]) for m in maps])), 1),
+               "replay_tokens_per_s": {"dense": round(tokens / (dense_total * 1e-6), 1),
+                                       "sparse": round(tokens / (sparse_total * 1e-6), 1),
+                                       "throughput_speedup": round(dense_total / sparse_total, 3)},
+               "reference_a100x_replay_tokens_per_s": {"dense": round(tokens / (ref_dense_ms * 1e-3), 1),
+                                                       "sparse": round(tokens / (ref_sparse_ms * 1e-3), 1),
+                                                       "throughput_speedup": round(ref_dense_ms / ref_sparse_ms, 3)}}
         results.append(row)
         log(json.dumps(row))
     line = {
