@@ -220,6 +220,26 @@ def cpu_baseline(point, seconds):
     }
 
 
+def cpu_point_us(point, runs=5):
+    """The same op on the oracle's CPU path (torch CPU gather + fp32 matmul, every host core): the
+    median of a few runs after one warm-up, shown beside each point's GPU time."""
+    import torch
+
+    from oracle import bsg_oracle as orc
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    x = torch.from_numpy(point.x_np)
+    w = torch.from_numpy(point.w_kn_np)
+    idx = torch.from_numpy(point.idx_np.astype("int64"))
+    orc.gemm_ref_torch(x, w, idx)
+    samples = []
+    for _ in range(runs):
+        t = time.perf_counter_ns()
+        orc.gemm_ref_torch(x, w, idx)
+        samples.append((time.perf_counter_ns() - t) / 1e3)
+    return statistics.median(samples)
+
+
 def load_traffic(point):
     """HBM bytes per launch of a roofline point, from its committed PMC summary (a line
     `traffic_bytes_per_launch: <int>`), or None when that point has no summary."""
@@ -803,6 +823,9 @@ def main():
     if not args.no_cpu and not args.only:
         log("cpu baseline ...")
         cpu = cpu_baseline(fp, args.cpu_seconds)
+        for p, row in zip(points, out_points):
+            row["cpu_us_per_gemm"] = round(cpu_point_us(p), 1)
+            row["gpu_speedup_over_cpu"] = round(row["cpu_us_per_gemm"] / row["us_per_gemm"], 1)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
