@@ -322,17 +322,26 @@ __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = blockIdx.x;
 
+  // Up to U 16-byte groups per thread are loaded before any is summed, so a batch of up to
+  // 32 * U rows costs one memory round trip rather than one per 32 rows.
+  constexpr int U = 4;
   uint64_t acc = 0;
   const int groups = p.bt * 8;
-  for (int gi = tid; gi < groups; gi += 256) {
-    const int row = gi >> 3;
-    const int col = 64 * j + 8 * (gi & 7);
-    if (col < p.K) {
-      const u32x4 v = *(const u32x4*)(p.x + (size_t)row * (size_t)p.ldx + col);
-      acc += f16_units(v.x & 0xffffu) + f16_units(v.x >> 16) + f16_units(v.y & 0xffffu) +
-             f16_units(v.y >> 16) + f16_units(v.z & 0xffffu) + f16_units(v.z >> 16) +
-             f16_units(v.w & 0xffffu) + f16_units(v.w >> 16);
+  for (int g0 = 0; g0 < groups; g0 += 256 * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gi = g0 + 256 * u + tid;
+      const int row = gi >> 3;
+      const int col = 64 * j + 8 * (gi & 7);
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (gi < groups && col < p.K) v[u] = *(const u32x4*)(p.x + (size_t)row * (size_t)p.ldx + col);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      acc += f16_units(v[u].x & 0xffffu) + f16_units(v[u].x >> 16) + f16_units(v[u].y & 0xffffu) +
+             f16_units(v[u].y >> 16) + f16_units(v[u].z & 0xffffu) + f16_units(v[u].z >> 16) +
+             f16_units(v[u].w & 0xffffu) + f16_units(v[u].w >> 16);
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
