@@ -430,15 +430,19 @@ __device__ __forceinline__ void part_emit(const GemmParams& p, size_t tile_lin, 
   part_store(dst + 192, v.w);
 }
 
-// Split-K hand-off: publish this work-group's partials, count arrivals; the last work-group
-// of the tile reduces the FT fragments in split order and re-arms the counter for the next
+// Split-K hand-off: publish this work-group's partials, count arrivals; in the last work-group
+// of the tile each wave that holds accumulators (every wave of kind 2, the first channel half
+// of kind 4, wave 0 of kind 1 after its in-group reduction) reduces its own fragments in split
+// order, taking this work-group's split from registers and loading only the other S - 1 (up to
+// 16 fragment loads in flight per round trip), stores Y and re-arms the counter for the next
 // launch (graph-replay safe).  Partials move through agent-scope (device-coherent) stores and
 // loads, so no L2 write-back/invalidate is needed: each wave waits for its own stores, the
 // barrier orders them before the counter update, and the last work-group loads only after it
-// has seen the final count.
-template <typename T, int FT, int CS, int WPG>
-__device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_lin, int y0, int n0, int w,
-                                              int* s_flag) {
+// has seen the final count.  wc = the wave's column group, CS = 16-column subtiles per tile,
+// FT = fragments per tile.
+template <typename T, int BTT, int NSUB, int CS, int FT>
+__device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_lin, int y0, int n0, int sk,
+                                              int wc, bool holds, const f32x4 (&acc)[BTT][NSUB], int* s_flag) {
   const int S = p.split_k;
   const int lane = threadIdx.x & 63;
   part_publish();
@@ -449,36 +453,44 @@ __device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_l
   }
   __syncthreads();
   if (!*s_flag) return;
-  // Work items (fragment, split) of this wave are requested 16 at a time before any is
-  // consumed (one memory round trip per 16), then summed per fragment in split order.
-  const float* base = (const float*)p.part + (tile_lin * S) * FT * 256 + lane;
-  constexpr int FW = (FT + WPG - 1) / WPG;  // fragments per wave
-  f32x4 acc2[FW];
+  if (holds) {
+    constexpr int F = BTT * NSUB;
+    constexpr int QB = F >= 16 ? 1 : 16 / F;  // splits per round trip
+    const float* base = (const float*)p.part + (tile_lin * S) * FT * 256 + lane;
+    f32x4 sum[BTT][NSUB];
 #pragma unroll
-  for (int i = 0; i < FW; ++i) acc2[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int items = FW * S;
-  for (int i0 = 0; i0 < items; i0 += 16) {
-    f32x4 t[16];
+    for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int it = i0 + i;
-      const int fi = it / S, q = it - fi * S, g = w + fi * WPG;
-      if (it < items && g < FT) t[i] = part_load(base + ((size_t)q * FT + g) * 256);
-    }
+      for (int s = 0; s < NSUB; ++s) sum[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q0 = 0; q0 < S; q0 += QB) {
+      f32x4 t[QB][BTT][NSUB];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int it = i0 + i;
-      const int fi = it / S, g = w + fi * WPG;
-      if (it < items && g < FT) {
+      for (int qq = 0; qq < QB; ++qq) {
+        const int q = q0 + qq;
+        if (q < S && q != sk) {
 #pragma unroll
-        for (int j = 0; j < FW; ++j)
-          if (j == fi) acc2[j] += t[i];
+          for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s)
+              t[qq][bi][s] = part_load(base + ((size_t)q * FT + bi * CS + wc * NSUB + s) * 256);
+        }
+      }
+#pragma unroll
+      for (int qq = 0; qq < QB; ++qq) {
+        const int q = q0 + qq;
+        if (q < S) {
+#pragma unroll
+          for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s) sum[bi][s] += q == sk ? acc[bi][s] : t[qq][bi][s];
+        }
       }
     }
-  }
 #pragma unroll
-  for (int j = 0; j < FW; ++j)
-    if (w + j * WPG < FT) store_y<T, CS>(p, y0, n0, w + j * WPG, acc2[j]);
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) store_y<T, CS>(p, y0, n0, bi * CS + wc * NSUB + s, sum[bi][s]);
+  }
   if (threadIdx.x == 0) counter_reset(&p.cnt[tile_lin]);
 }
 
@@ -607,9 +619,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
-          f32x4 v = acc[bi][s];
-          for (int ww = 1; ww < WPG; ++ww) v += s_red[((ww - 1) * F + bi * NSUB + s) * 64 + lane];
-          emit(bi * NSUB + s, v);
+          for (int ww = 1; ww < WPG; ++ww) acc[bi][s] += s_red[((ww - 1) * F + bi * NSUB + s) * 64 + lane];
+          emit(bi * NSUB + s, acc[bi][s]);
         }
     }
   } else {
@@ -619,7 +630,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
   }
 
-  if (S > 1) splitk_finish<T, F, NSUB, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
+  if (S > 1) splitk_finish<T, BTT, NSUB, NSUB, F>(p, tile_lin, y0, n0y, sk, 0, w == 0, acc, &s_misc[WPG]);
 }
 
 // Kinds 2 and 4 ("xlds"): one work-group = BTT*16 batch rows x WC*NSUB*16 columns; its waves
@@ -762,7 +773,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
           part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
       }
   }
-  if (S > 1) splitk_finish<T, FT, CS, WPG>(p, tile_lin, y0, n0y, w, &s_misc[WPG]);
+  if (S > 1) splitk_finish<T, BTT, NSUB, CS, FT>(p, tile_lin, y0, n0y, sk, wc, wk == 0, acc, &s_misc[WPG]);
 }
 
 // Kind 3 ("fma", batch tiles of 1-8 rows): the contraction is too thin for MFMA, so each lane
