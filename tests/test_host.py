@@ -55,6 +55,38 @@ def test_lookup_from_custom_table(tmp_path):
         tuning.load_table()
 
 
+class _ScriptedCase:
+    """Stands in for tuning._Case: each plan returns its scripted timings in turn."""
+
+    def __init__(self, times):
+        self.times = {k: list(v) for k, v in times.items()}
+        self.calls = []
+
+    def time(self, plan, dense=False):
+        key = plan.as_tuple()
+        self.calls.append(key)
+        v = self.times[key].pop(0)
+        if v is None:
+            raise bsa.BsgUnsupported(-5, "not instantiated")
+        return v
+
+
+def test_tuner_retimes_close_candidates():
+    a, b, c, d = (bsa.Plan(1, 16, 2, 4, 16, 1), bsa.Plan(1, 16, 4, 4, 16, 1), bsa.Plan(2, 32, 2, 4, 16, 1),
+                  bsa.Plan(1, 64, 2, 4, 16, 1))
+    # b's single first timing is lucky; a is faster on the median of four; c is out of the 5%
+    # margin and never re-timed; d is rejected by the library
+    case = _ScriptedCase({a.as_tuple(): [5.0, 4.8, 4.9, 4.85], b.as_tuple(): [4.9, 5.6, 5.5, 5.7],
+                          c.as_tuple(): [6.0], d.as_tuple(): [None]})
+    us, plan = tuning._pick(case, [a, b, c, d])
+    assert plan.as_tuple() == a.as_tuple() and us == pytest.approx(4.875)
+    assert case.calls.count(c.as_tuple()) == 1 and case.calls.count(b.as_tuple()) == 4
+    # a lone finalist is taken on its first timing; nothing runnable gives (inf, None)
+    case = _ScriptedCase({a.as_tuple(): [5.0], c.as_tuple(): [6.0]})
+    assert tuning._pick(case, [a, c]) == (5.0, a)
+    assert tuning._pick(_ScriptedCase({d.as_tuple(): [None]}), [d]) == (float("inf"), None)
+
+
 def test_reference_lookup_both_key_sets(tmp_path):
     pkc = {"down": {"0.5": {"mask": "bitmap", "block_k": 64, "K": 4, "tile": [16, 64, 2, 3],
                             "dense_ms": 0.05, "sparse_ms": 0.03, "speedup": 1.6},

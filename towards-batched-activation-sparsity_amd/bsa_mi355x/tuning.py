@@ -228,6 +228,26 @@ def _time_or_inf(case: "_Case", plan: Plan, dense: bool = False) -> float:
         return float("inf")
 
 
+def _pick(case: "_Case", plans: Sequence[Plan], dense: bool = False, margin: float = 0.05, finalists: int = 4,
+          rounds: int = 3) -> Tuple[float, Optional[Plan]]:
+    """Best plan for a case: every candidate is timed once; those within `margin` of the best
+    (at most `finalists`) are timed `rounds` more times, interleaved, and the lowest median wins
+    (one timing each lets plans a few percent apart swap places from run to run)."""
+    first = sorted(((us, p) for p in plans for us in [_time_or_inf(case, p, dense=dense)] if math.isfinite(us)),
+                   key=lambda t: t[0])
+    if not first:
+        return float("inf"), None
+    fin = [t for t in first if t[0] <= first[0][0] * (1.0 + margin)][:finalists]
+    if len(fin) == 1:
+        return fin[0]
+    samples = [[us] for us, _ in fin]
+    for _ in range(rounds):
+        for i, (_, p) in enumerate(fin):
+            samples[i].append(case.time(p, dense=dense))
+    i = min(range(len(fin)), key=lambda j: statistics.median(samples[j]))
+    return statistics.median(samples[i]), fin[i][1]
+
+
 def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densities: Sequence[float],
          out_table: str = TABLE_PATH, lookup_dir: Optional[str] = None, rotate_bytes: int = 1 << 30,
          seed: int = 1234, log=print, merge_from: Optional[str] = None) -> List[dict]:
@@ -244,22 +264,14 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
         nblk = (k + BLOCK_K - 1) // BLOCK_K
         for bt in batch_sizes:
             case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes)
-            dense_best = (float("inf"), None)
-            for p in candidate_plans(bt, nblk, nblk):
-                us = _time_or_inf(case, p, dense=True)
-                if us < dense_best[0]:
-                    dense_best = (us, p)
+            dense_best = _pick(case, candidate_plans(bt, nblk, nblk), dense=True)
             entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": nblk, "dense": True,
                             "plan": list(dense_best[1].as_tuple()), "us": round(dense_best[0], 3)})
             gen = torch.Generator().manual_seed(seed)
             for d in densities:
                 na = max(1, min(nblk, int(math.floor(float(d) * nblk))))
                 case.idx = torch.randperm(nblk, generator=gen)[:na].sort()[0].to(torch.int32).to(dev)
-                best = (float("inf"), None)
-                for p in candidate_plans(bt, na, nblk):
-                    us = _time_or_inf(case, p)
-                    if us < best[0]:
-                        best = (us, p)
+                best = _pick(case, candidate_plans(bt, na, nblk))
                 entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": na, "dense": False,
                                 "plan": list(best[1].as_tuple()), "us": round(best[0], 3)})
                 t = best[1]
