@@ -223,6 +223,24 @@ def test_pack_layout_bit_exact(dev):
         assert np.array_equal(got_kn.view(np.uint16), want.view(np.uint16)), (n, k, "kn")
 
 
+@pytest.mark.parametrize("plan", [(8, 16, 2, 4, 16, 1), (8, 16, 4, 4, 16, 2), (8, 16, 8, 4, 64, 4), (8, 32, 8, 4, 64, 4)])
+def test_split_k_more_splits_than_blocks(dev, plan):
+    """Split-K 8 over 3 (then 1, then 0) active blocks: most work-groups' slices are empty, so
+    the last arriver's own split is often all zeros and it loads the others'.  One workspace
+    for every call, so each call also checks that the previous one re-armed the counters."""
+    bt, k, n = 40, 4096, 1000
+    x, w_nk, idx = case(29, bt, k, n, 3)
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    pl = bsa.Plan(*plan)
+    for sub in (idx, idx[1:2], idx[:0]):
+        out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        print(f"split-K 8 plan={plan} na={len(sub)}", flush=True)
+        bsa.gemm_packed(xt, packed, n, to_dev(np.ascontiguousarray(sub), dev), out, plan=pl, workspace_prefix="sk_sparse")
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), orc.gemm_ref(x, w_nk, sub), f"plan {plan} na={len(sub)}")
+
+
 def test_deterministic_repeats(dev):
     bt, k, n, na = 16, 11008, 4096, 62
     x, w_nk, idx = case(16, bt, k, n, na)
