@@ -87,6 +87,25 @@ def test_tuner_retimes_close_candidates():
     assert tuning._pick(_ScriptedCase({d.as_tuple(): [None]}), [d]) == (float("inf"), None)
 
 
+def test_lookup_row_groups_only_as_tuned(tmp_path):
+    """A 64-row-bucket batch may run two 32-row groups (tuned so); a 16-row tile never serves
+    a larger batch."""
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"entries": [
+        {"bt": 64, "N": 4096, "K": 4096, "na": 30, "dense": False, "plan": [1, 32, 2, 4, 32, 1], "us": 1.0},
+        {"bt": 64, "N": 4096, "K": 4096, "na": 40, "dense": False, "plan": [1, 16, 2, 4, 16, 1], "us": 1.0},
+    ]}))
+    tuning.load_table(str(path))
+    try:
+        assert tuning.lookup(64, 4096, 64, 30).as_tuple() == (1, 32, 2, 4, 32, 1)
+        assert tuning.lookup(48, 4096, 64, 30).as_tuple() == (1, 32, 2, 4, 32, 1)
+        assert tuning.lookup(64, 4096, 64, 40) is None
+    finally:
+        tuning.load_table()
+    rows = {p.rows_per_group for p in tuning.candidate_plans(64, 30, 64)}
+    assert rows == {32, 64}
+
+
 def test_reference_lookup_both_key_sets(tmp_path):
     pkc = {"down": {"0.5": {"mask": "bitmap", "block_k": 64, "K": 4, "tile": [16, 64, 2, 3],
                             "dense_ms": 0.05, "sparse_ms": 0.03, "speedup": 1.6},
