@@ -100,10 +100,12 @@ def test_lookup_row_groups_only_as_tuned(tmp_path):
         assert tuning.lookup(64, 4096, 64, 30).as_tuple() == (1, 32, 2, 4, 32, 1)
         assert tuning.lookup(48, 4096, 64, 30).as_tuple() == (1, 32, 2, 4, 32, 1)
         assert tuning.lookup(64, 4096, 64, 40) is None
+        assert tuning.lookup(32, 4096, 64, 40) is None        # no 32-row-bucket entry
     finally:
         tuning.load_table()
-    rows = {p.rows_per_group for p in tuning.candidate_plans(64, 30, 64)}
-    assert rows == {32, 64}
+    assert {p.rows_per_group for p in tuning.candidate_plans(64, 30, 64)} == {32, 64}
+    assert {p.rows_per_group for p in tuning.candidate_plans(32, 30, 64)} == {16, 32, 64}
+    assert {p.rows_per_group for p in tuning.candidate_plans(16, 30, 64)} == {16}
 
 
 def test_reference_lookup_both_key_sets(tmp_path):

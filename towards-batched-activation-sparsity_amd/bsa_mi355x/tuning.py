@@ -80,9 +80,9 @@ def lookup(bt: int, n: int, nblk: int, na: int, dense: bool = False) -> Optional
         return None
     e = min(same, key=lambda e: (abs(int(e["na"]) - na), int(e["na"])))
     p = Plan(*[int(v) for v in e["plan"]])
-    # a plan may split the batch into row groups only as it was tuned: 32-row groups in the
-    # 64-row bucket; never a smaller tile than the batch's own bucket otherwise
-    if p.rows_per_group < min(bt, 64) and not (rb == 64 and p.rows_per_group == 32):
+    # a plan may split the batch into row groups only as it was tuned: groups of half the
+    # bucket's rows (16 in the 32-row bucket, 32 in the 64-row one); never smaller tiles
+    if p.rows_per_group < min(bt, 64) and not (rb >= 32 and p.rows_per_group == rb // 2):
         return None
     return p
 
@@ -157,9 +157,10 @@ def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
             if rows == fma_rows:
                 out.append(Plan(1, cols, waves, depth, rows, kind))
             continue
-        # 32-row batches also try 64-row tiles; 64-row batches also try two 32-row groups, which
-        # read each weight block twice, concurrently, but fill the chip without split-K
-        if rows != rb and not (rb == 32 and rows == 64) and not (rb == 64 and rows == 32):
+        # 32-row batches also try 64-row tiles; 32- and 64-row batches also try two row groups of
+        # half the rows, which read each weight block twice, concurrently, but fill the chip
+        # without split-K
+        if rows != rb and not (rb == 32 and rows == 64) and not (rb >= 32 and rows == rb // 2):
             continue
         for sk in (1, 2, 3, 4, 6, 8):
             if sk * (waves if kind == 1 else 1) > max(na, 1):
