@@ -317,8 +317,17 @@ struct SelParams {
 // integer units, and stores it.  The ranking (bsg_rank_l1_kernel, or a GEMM in top-k mode) is a
 // separate launch: a last-arriver hand-off would put every work-group's increment on one
 // device-scope counter, and those serialize (4-7 us at 64-172 blocks, measured).
+// One DPP row shift (row_shr:n = 0x110 + n) of a 64-bit value: lane i of each 16-lane row
+// reads lane i - n of the same row, and 0 where that lane lies outside the row.
+template <int CTRL>
+__device__ __forceinline__ uint64_t u64_row_shr(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, CTRL, 0xf, 0xf, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), CTRL, 0xf, 0xf, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
-  __shared__ uint64_t s_part[4];
+  __shared__ uint64_t s_part[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = blockIdx.x;
 
@@ -343,11 +352,20 @@ __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
              f16_units(v[u].y >> 16) + f16_units(v[u].z & 0xffffu) + f16_units(v[u].z >> 16) +
              f16_units(v[u].w & 0xffffu) + f16_units(v[u].w >> 16);
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
-  if (lane == 0) s_part[w] = acc;
+  // Inclusive scan within each 16-lane row (a few cycles per step, no LDS round trip): lane 15
+  // of every row ends with the row's sum; the 16 row sums of the work-group meet in LDS.
+  acc += u64_row_shr<0x111>(acc);
+  acc += u64_row_shr<0x112>(acc);
+  acc += u64_row_shr<0x114>(acc);
+  acc += u64_row_shr<0x118>(acc);
+  if ((lane & 15) == 15) s_part[4 * w + (lane >> 4)] = acc;
   __syncthreads();
-  if (tid == 0) p.scores[j] = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+  if (tid == 0) {
+    uint64_t t = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += s_part[i];
+    p.scores[j] = t;
+  }
 }
 
 // One work-group after bsg_score_l1_kernel on the same stream (the launch boundary orders the
