@@ -1,19 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X batch-shared block-sparse GEMM (one JSON line on stdout).
 
-Workload: Llama-2-7B down_proj, B=16, K=11008 (172 blocks of 64),
-N=4096, fp16, sweeping block sparsity {0, 0.25, 0.5, 0.638, 0.8}; the 0% point runs the same
-kernel with every block active (the in-run dense baseline).  One "step" = one replay of a
-hipGraph holding every sweep point's R back-to-back GEMM launches, each on a different copy of
-the packed weight (R copies span >= 1 GiB, so the 256 MB Infinity Cache cannot serve a repeat
-and the bytes really come from HBM).  Per-point µs/GEMM come from each point's own graph.
+Default workload (the configuration the headline metric is quoted on):
+every Llama-2-7B decoder projection shape -- q/k/v/o (K=4096 -> N=4096), gate/up (4096 -> 11008),
+down (11008 -> 4096) -- at B=2 with block sparsity 0.803, B=16 at 0.638 and B=64 at 0.520, fp16,
+each beside the same kernel with every block active (the in-run dense baseline).  The down_proj
+B=16 sparsity sweep of configs[1] ({0, 0.25, 0.5, 0.638, 0.8}) rides along as extra points; its
+s=0.5 point is the CPU-reference configuration of configs[0].
 
-value  = active-weight bytes of all GEMMs in the timed steps / timed seconds (GB/s)
-roofline = the s=0.5 sparse GEMM (86/172 blocks): algorithmic bytes na*64*N*2 per launch over
-           the average launch duration from HIP events around its graph replays.
-cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul) on the s=0.5 point.
+Rotation: one pool of packed-weight copies per projection shape.  A point's graph holds R
+back-to-back launches, launch i reading copy i, with R = ceil(1 GiB / the point's ACTIVE weight
+bytes), so every replay streams at least 1 GiB of distinct active weight and the 256 MB Infinity
+Cache cannot serve a repeat.  A "step" is one replay of a graph holding every point's R launches.
 
-    python bench.py [--steps K] [--warmup W] [--workload down_sweep|llama|fused|decode|perstep]
+value        = active-weight bytes of all GEMMs in the timed steps / timed seconds (GB/s)
+roofline     = the gate/up B=64 s=0.52 GEMM, the largest sparse point: algorithmic bytes
+               na*64*N*2 per launch over the average launch duration, from HIP events on the
+               launch stream around that point's graph replays
+cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host core) on the
+               configs[0] point, down_proj B=16 with 86 of 172 blocks; every point also carries
+               its own CPU time
+
+    python bench.py [--steps K] [--warmup W]
+                    [--workload llama|down_sweep|fused|decode|perstep|2d] [--only POINT]
 """
 from __future__ import annotations
 
@@ -34,12 +43,18 @@ for _p in (PKG_ROOT, ROOT):
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 1 << 30
+SEED = 1234
 METRIC = "µs/GEMM + HBM GB/s + speedup vs dense, Llama-2-7B shapes at B=2/16/64"
+# (K, N) of the Llama-2-7B projection shapes and the input distribution of each
+SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
+X_DIST = {"qkvo": "normal", "gate_up": "normal", "down": "laplace"}
 # Committed PMC summaries (HBM bytes per launch) of the roofline point of each workload.
 TRAFFIC_PROFILES = {
     "down_b16_s500": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md"),
     "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_xl_gate_up_b64_s520.md"),
 }
+# Kernel (symbol prefix) that each plan kind launches.
+KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel"}
 
 
 def log(msg: str) -> None:
@@ -51,8 +66,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="down_sweep",
-                    choices=["down_sweep", "llama", "fused", "decode", "perstep", "2d"])
+    ap.add_argument("--workload", default="llama",
+                    choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d"])
     ap.add_argument("--batches", default=None, help="perstep workload: batch sizes (default: all six)")
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
@@ -63,59 +78,84 @@ def parse_args():
     return ap.parse_args()
 
 
-class Point:
-    """One GEMM configuration: packed weight copies + a graph of R rotated launches."""
+def copies_for(active_bytes: int) -> int:
+    """Launches per graph so that one replay reads >= ROTATE_BYTES of distinct active weight."""
+    return max(1, math.ceil(ROTATE_BYTES / max(1, int(active_bytes))))
 
-    def __init__(self, name, bt, k, n, na, x_dist, seed, dev, dense=False, plan=None):
+
+class ShapePool:
+    """Packed-weight copies of one projection shape.  W is the first draw of
+    numpy default_rng(seed) -- N(0, 0.02) stored [K, N], fp16 -- exactly as oracle.make_inputs
+    draws it, so every point of this shape sees the same W as its oracle inputs."""
+
+    def __init__(self, name, k, n, dev, copies, seed=SEED):
         import numpy as np
+        import torch
+
+        import bsa_mi355x as bsa
+
+        self.name, self.k, self.n, self.dev = name, k, n, dev
+        self.nblk = (k + 63) // 64
+        rng = np.random.default_rng(seed)
+        self.w_kn_np = rng.normal(0.0, 0.02, size=(k, n)).astype(np.float16)
+        w0 = torch.from_numpy(self.w_kn_np).to(dev)
+        p0 = bsa.pack_weight(w0, layout="kn")
+        del w0
+        self.copies = max(1, int(copies))
+        self.packed = [p0] + [p0.clone() for _ in range(self.copies - 1)]
+        self.packed_bytes = p0.numel() * p0.element_size()
+        self._kn = None
+
+    def w_kn(self, count):
+        """`count` [K, N] copies of W (hipBLASLt context), made on first use."""
+        import torch
+
+        if self._kn is None or len(self._kn) < count:
+            w0 = torch.from_numpy(self.w_kn_np).to(self.dev)
+            self._kn = [w0] + [w0.clone() for _ in range(count - 1)]
+        return self._kn[:count]
+
+
+class Point:
+    """One GEMM configuration on a shape pool: its inputs, plan and a graph of R rotated launches."""
+
+    def __init__(self, name, pool, bt, na, dev, dense=False, plan=None, inputs=None, seed=SEED):
         import torch
 
         import bsa_mi355x as bsa
         from oracle import bsg_oracle as orc
 
-        self.name, self.bt, self.k, self.n, self.na, self.dense = name, bt, k, n, na, dense
-        nb = orc.nblk_of(k)
-        self.nblk = nb
-        x, w_kn, idx = orc.make_inputs(seed, bt, k, n, x_dist, na=(nb if dense else na))
-        self.x_np, self.w_kn_np, self.idx_np = x, w_kn, idx
+        self.name, self.pool, self.bt, self.dense = name, pool, bt, dense
+        self.k, self.n, self.nblk = pool.k, pool.n, pool.nblk
+        self.na = pool.nblk if dense else na
+        if inputs is None:
+            # x, then the mask, from oracle.make_inputs' rng stream (W is drawn first, as the pool's)
+            x, _, idx = orc.make_inputs(seed, bt, self.k, self.n, X_DIST[pool.name], na=self.na)
+        else:
+            x, idx = inputs
+        self.x_np, self.idx_np = x, idx
         self.x = torch.from_numpy(x).to(dev)
-        w_kn_t = torch.from_numpy(w_kn).to(dev)
-        packed = bsa.pack_weight(w_kn_t, layout="kn")
-        del w_kn_t
-        self.copies = max(1, math.ceil(ROTATE_BYTES / packed.numel() / 2))
-        self.packed = [packed] + [packed.clone() for _ in range(self.copies - 1)]
         self.idx = torch.from_numpy(idx).to(dev)
-        self.y = torch.empty(bt, n, dtype=torch.float16, device=dev)
-        self.plan = bsa.resolve_plan(bt, n, nb, nb if dense else na, dev, plan, dense=dense)
-        self.active_bytes = (nb if dense else na) * 64 * n * 2
-        self.flops = 2 * bt * (nb if dense else na) * 64 * n
+        self.y = torch.empty(bt, self.n, dtype=torch.float16, device=dev)
+        self.plan = bsa.resolve_plan(bt, self.n, self.nblk, self.na, dev, plan, dense=dense)
+        self.active_bytes = self.na * 64 * self.n * 2
+        self.flops = 2 * bt * self.na * 64 * self.n
+        self.copies = min(pool.copies, copies_for(self.active_bytes))
         self.graph = None
+
+    @property
+    def replay_bytes(self) -> int:
+        return self.active_bytes * self.copies
 
     def launch(self, i):
         import bsa_mi355x as bsa
 
-        p = self.packed[i % self.copies]
-        if self.dense:
-            bsa.gemm_packed(self.x, p, self.n, None, self.y, plan=self.plan, workspace_prefix=f"bench_{self.name}")
-        else:
-            bsa.gemm_packed(self.x, p, self.n, self.idx, self.y, plan=self.plan, workspace_prefix=f"bench_{self.name}")
+        p = self.pool.packed[i % self.copies]
+        bsa.gemm_packed(self.x, p, self.n, None if self.dense else self.idx, self.y, plan=self.plan,
+                        workspace_prefix=f"bench_{self.name}")
 
     def capture(self):
-        import torch
-
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for i in range(self.copies):
-                self.launch(i)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(self.copies):
-                self.launch(i)
-        torch.cuda.synchronize()
-        self.graph = g
+        self.graph = _capture([lambda i=i: self.launch(i) for i in range(self.copies)])
 
     def check(self):
         """Parity of the benchmarked launch against the oracle (fp32 CPU path)."""
@@ -126,31 +166,34 @@ class Point:
 
         self.launch(0)
         torch.cuda.synchronize()
-        w_nk = np.ascontiguousarray(self.w_kn_np.T)
+        w_nk = np.ascontiguousarray(self.pool.w_kn_np.T)
         ref = orc.gemm_ref(self.x_np, w_nk, self.idx_np)
         y = self.y.float().cpu().numpy()
         return orc.rel_frobenius(y, ref), orc.within_tolerance(y, ref)
 
 
-def capture_step(points):
-    """One hipGraph holding a whole step: every point's R rotated launches, back to back."""
+def _capture(fns):
+    """Warm up fns on a side stream (workspaces, plans), then capture them back to back as one graph."""
     import torch
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for p in points:
-            for i in range(p.copies):
-                p.launch(i)
+        for f in fns:
+            f()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for p in points:
-            for i in range(p.copies):
-                p.launch(i)
+        for f in fns:
+            f()
     torch.cuda.synchronize()
     return g
+
+
+def capture_step(points):
+    """One hipGraph holding a whole step: every point's R rotated launches, back to back."""
+    return _capture([lambda p=p, i=i: p.launch(i) for p in points for i in range(p.copies)])
 
 
 def time_points(points, step_graph, steps, warmup, reps=10):
@@ -189,34 +232,55 @@ def time_points(points, step_graph, steps, warmup, reps=10):
     return total_ms, wall, per
 
 
+def _cpu_tensors(point):
+    import torch
+
+    x = torch.from_numpy(point.x_np)
+    w = torch.from_numpy(point.pool.w_kn_np)
+    idx = torch.from_numpy(point.idx_np.astype("int64"))
+    return x, w, idx
+
+
 def cpu_baseline(point, seconds):
+    """The oracle's CPU path on the GPU box's host cores: gather + convert + fp32 matmul, and the
+    matmul alone on already gathered fp32 operands, each timed for about `seconds`."""
     import torch
 
     from oracle import bsg_oracle as orc
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    x = torch.from_numpy(point.x_np)
-    w = torch.from_numpy(point.w_kn_np)
-    idx = torch.from_numpy(point.idx_np.astype("int64"))
-    for _ in range(2):
-        orc.gemm_ref_torch(x, w, idx)
-    samples = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end and len(samples) < 500:
-        t = time.perf_counter_ns()
-        orc.gemm_ref_torch(x, w, idx)
-        samples.append((time.perf_counter_ns() - t) / 1e3)
-    us = statistics.median(samples)
+    x, w, idx = _cpu_tensors(point)
+
+    def sample(fn, budget):
+        for _ in range(2):
+            fn()
+        out = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end and len(out) < 500:
+            t = time.perf_counter_ns()
+            fn()
+            out.append((time.perf_counter_ns() - t) / 1e3)
+        return out
+
+    full = sample(lambda: orc.gemm_ref_torch(x, w, idx), seconds * 0.7)
+    cols = (64 * idx[:, None] + torch.arange(64)[None, :]).reshape(-1)
+    xa = x.index_select(1, cols).float()
+    wa = w.index_select(0, cols).float()
+    mm = sample(lambda: xa @ wa, seconds * 0.3)
+    us = statistics.median(full)
+    us_mm = statistics.median(mm)
     return {
         "value": round(point.active_bytes / (us * 1e-6) / 1e9, 2),
         "unit": "GB/s",
         "us_per_gemm": round(us, 1),
+        "matmul_only": {"us_per_gemm": round(us_mm, 1),
+                        "GBps": round(point.active_bytes / (us_mm * 1e-6) / 1e9, 2), "runs": len(mm)},
         "cores": cores,
         "kind": "port",
         "sample": (f"oracle gemm_ref_torch (torch CPU gather + fp32 matmul) on {point.name}: B={point.bt} "
-                   f"K={point.k} N={point.n} {point.na}/{point.nblk} blocks; {len(samples)} timed runs after 2 "
-                   f"warm-ups, median"),
+                   f"K={point.k} N={point.n} {point.na}/{point.nblk} blocks; {len(full)} timed runs after 2 "
+                   f"warm-ups, median; matmul_only = the fp32 matmul on pre-gathered operands"),
     }
 
 
@@ -228,9 +292,7 @@ def cpu_point_us(point, runs=5):
     from oracle import bsg_oracle as orc
 
     torch.set_num_threads(len(os.sched_getaffinity(0)))
-    x = torch.from_numpy(point.x_np)
-    w = torch.from_numpy(point.w_kn_np)
-    idx = torch.from_numpy(point.idx_np.astype("int64"))
+    x, w, idx = _cpu_tensors(point)
     orc.gemm_ref_torch(x, w, idx)
     samples = []
     for _ in range(runs):
@@ -275,31 +337,14 @@ def copy_calibration(mib, steps):
 
 
 def torch_mm_us(point, reps=5):
-    """hipBLASLt dense GEMM (torch.mm) on the same shape, rotated over weight copies: context."""
+    """hipBLASLt dense GEMM (torch.mm) on the same shape, rotated over [K, N] weight copies
+    (>= 1 GiB per replay): context for the dense points."""
     import torch
 
-    w0 = torch.from_numpy(point.w_kn_np).to(point.x.device)
-    ws = [w0] + [w0.clone() for _ in range(point.copies - 1)]
+    ws = point.pool.w_kn(copies_for(point.pool.packed_bytes))
     out = torch.empty(point.bt, point.n, dtype=torch.float16, device=point.x.device)
-    torch.mm(point.x, ws[0], out=out)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for w in ws:
-            torch.mm(point.x, w, out=out)
-    g.replay()
-    torch.cuda.synchronize()
-    ts = []
-    for _ in range(reps):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        g.replay()
-        b.record()
-        b.synchronize()
-        ts.append(a.elapsed_time(b) * 1000.0 / len(ws))
-    del g, ws
-    return statistics.median(ts)
+    med, _ = _graph_time([lambda w=w: torch.mm(point.x, w, out=out) for w in ws], reps)
+    return med / len(ws)
 
 
 def read_calibration_us(point, reps=5):
@@ -316,7 +361,7 @@ def read_calibration_us(point, reps=5):
 
     def launch(i):
         def f():
-            rc = lib.bsg_read_calibrate(point.packed[i].data_ptr(), nbytes, sink.data_ptr(),
+            rc = lib.bsg_read_calibrate(point.pool.packed[i].data_ptr(), nbytes, sink.data_ptr(),
                                         torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(lib.bsg_last_error().decode())
@@ -326,24 +371,11 @@ def read_calibration_us(point, reps=5):
     return med / point.copies
 
 
-KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel"}
-
-
 def _graph_time(fns, reps, warmup=2):
-    """Capture fns back to back as one graph; median µs per replay over `reps` replays."""
+    """Capture fns back to back as one graph; median and mean µs per replay over `reps` replays."""
     import torch
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for f in fns:
-            f()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for f in fns:
-            f()
+    g = _capture(fns)
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -356,41 +388,213 @@ def _graph_time(fns, reps, warmup=2):
         b.record()
         b.synchronize()
         ts.append(a.elapsed_time(b) * 1000.0)
+    del g
     return statistics.median(ts), statistics.mean(ts)
+
+
+def sname(s: float) -> str:
+    return f"s{int(round(s * 1000)):03d}"
+
+
+def matrix_points(workload, dev):
+    """The points of the llama (configs[2] + the configs[1] sweep) or down_sweep workload:
+    [(name, shape, B, na, dense)]."""
+    from oracle import bsg_oracle as orc
+
+    rows = []
+    if workload == "llama":
+        for bt, s in ((2, 0.803), (16, 0.638), (64, 0.520)):
+            for sh, (k, _) in SHAPES.items():
+                nb = orc.nblk_of(k)
+                rows.append((f"{sh}_b{bt}_{sname(s)}", sh, bt, orc.n_active_for_sparsity(s, nb), False))
+                rows.append((f"{sh}_b{bt}_dense", sh, bt, nb, True))
+    # configs[1]: down_proj B=16 over {0, 0.25, 0.5, 0.638, 0.8} (0.638 and 0 are in configs[2])
+    have = {r[0] for r in rows}
+    nb = orc.nblk_of(SHAPES["down"][0])
+    for s in (0.0, 0.25, 0.5, 0.638, 0.8):
+        name = "down_b16_dense" if s == 0.0 else f"down_b16_{sname(s)}"
+        if name not in have:
+            rows.append((name, "down", 16, nb if s == 0.0 else orc.n_active_for_sparsity(s, nb), s == 0.0))
+    return rows
+
+
+def pool_copies(rows):
+    """Copies of each shape's packed weight: enough for its point with the fewest active bytes
+    to read >= ROTATE_BYTES of distinct weight per replay (every other point uses a prefix)."""
+    need = {}
+    for _, sh, _, na, _ in rows:
+        need[sh] = max(need.get(sh, 1), copies_for(na * 64 * SHAPES[sh][1] * 2))
+    return need
+
+
+def run_matrix(args, dev):
+    import torch
+
+    rows = matrix_points(args.workload, dev)
+    if args.only:
+        rows = [r for r in rows if r[0] == args.only]
+        if not rows:
+            raise SystemExit(f"--only {args.only}: no such point")
+    need = pool_copies(rows)
+    pools = {sh: ShapePool(sh, *SHAPES[sh], dev, need[sh]) for sh in need}
+    log("weight pools: " + ", ".join(f"{p.name} x{p.copies} ({p.copies * p.packed_bytes / 1e9:.1f} GB)"
+                                     for p in pools.values()))
+    # X once per (shape, B) and every mask of that pair from the same stream (oracle.make_inputs)
+    from oracle import bsg_oracle as orc
+
+    drawn = {}
+    for key in dict.fromkeys((sh, bt) for _, sh, bt, _, _ in rows):
+        nas = sorted({na for _, s2, b2, na, _ in rows if (s2, b2) == key})
+        x, _, masks = orc.make_inputs(SEED, key[1], *SHAPES[key[0]], X_DIST[key[0]], na=nas)
+        drawn[key] = (x, dict(zip(nas, masks)))
+    points = []
+    for name, sh, bt, na, dense in rows:
+        x, masks = drawn[(sh, bt)]
+        points.append(Point(name, pools[sh], bt, na, dev, dense=dense, inputs=(x, masks[na])))
+        log(f"prepared {name}: na={points[-1].na} copies={points[-1].copies} "
+            f"replay={points[-1].replay_bytes / 2**30:.2f} GiB plan={points[-1].plan}")
+    bad = []
+    for p in points:
+        rf, ok = p.check()
+        if not ok:
+            bad.append((p.name, rf))
+    if bad:
+        raise SystemExit(f"parity failure before timing: {bad}")
+    log("parity ok on every point")
+    for p in points:
+        p.capture()
+    step_graph = capture_step(points)
+    log("graphs captured")
+
+    total_ms, wall, per = time_points(points, step_graph, args.steps, args.warmup)
+    step_bytes = sum(p.replay_bytes for p in points)
+    value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
+    log(f"timed {args.steps} steps in {total_ms:.2f} ms (host wall {wall * 1e3:.1f} ms)")
+
+    dense_us = {p.name[: -len("_dense")]: per[p.name][0] for p in points if p.dense}
+    out_points = []
+    for p in points:
+        med, mean = per[p.name]
+        gbs = p.active_bytes / (med * 1e-6) / 1e9
+        row = {"name": p.name, "B": p.bt, "K": p.k, "N": p.n, "active_blocks": p.na, "nblk": p.nblk,
+               "us_per_gemm": round(med, 3), "GBps_active": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+               "floor_us_at_8TBps": round(p.active_bytes / (HBM_PEAK_GBS * 1e3), 3),
+               "replay_GiB": round(p.replay_bytes / 2**30, 3), "plan": list(p.plan.as_tuple()),
+               "kernel": KERNEL_NAMES.get(p.plan.kind, "bsg_gemm")}
+        if p.bt >= 16:
+            # derived (flops / time / peak), not a counter reading
+            row["mfma_util_derived"] = round(p.flops / (med * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 5)
+        if not p.dense:
+            d = dense_us.get(p.name.rsplit("_s", 1)[0])
+            if d:
+                row["speedup_vs_dense"] = round(d / med, 3)
+                row["ideal_speedup"] = round(p.nblk / p.na, 3)
+                row["speedup_over_ideal"] = round((d / med) / (p.nblk / p.na), 3)
+        out_points.append(row)
+        log(json.dumps(row))
+
+    focus = "gate_up_b64_s520" if args.workload == "llama" else "down_b16_s500"
+    if args.only:
+        focus = points[0].name
+    fp = next(p for p in points if p.name == focus)
+    f_med, f_mean = per[focus]
+    achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(focus),
+                "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
+                "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes,
+                "plan": list(fp.plan.as_tuple())}
+    if not args.only:
+        rd = read_calibration_us(fp)
+        roofline["practical_read"] = {
+            "us_per_launch": round(rd, 3), "GBps": round(fp.active_bytes / (rd * 1e-6) / 1e9, 1),
+            "frac_of_it": round(rd / f_mean, 4),
+            "what": "bsg_read_calibrate streaming the same bytes per launch (weight-load pattern, no compute), "
+                    "same rotation and timing"}
+        log(f"practical read of {fp.active_bytes / 1e6:.2f} MB: {rd:.2f} us ({roofline['practical_read']['GBps']} GB/s)")
+        for p, row in zip(points, out_points):
+            if p.dense and p.bt == 16:
+                row["torch_mm_us"] = round(torch_mm_us(p), 3)
+                log(f"torch.mm (hipBLASLt) on {p.name}: {row['torch_mm_us']:.2f} us")
+    cpu = None
+    if not args.no_cpu and not args.only:
+        log("cpu baseline ...")
+        cpu_pt = next((p for p in points if p.name == "down_b16_s500"), fp)
+        cpu = cpu_baseline(cpu_pt, args.cpu_seconds)
+        for p, row in zip(points, out_points):
+            row["cpu_us_per_gemm"] = round(cpu_point_us(p), 1)
+            row["gpu_speedup_over_cpu"] = round(row["cpu_us_per_gemm"] / row["us_per_gemm"], 1)
+    sparse = [r for r in out_points if "speedup_over_ideal" in r]
+    if args.workload == "llama":
+        workload = ("Llama-2-7B q/k/v/o (4096->4096), gate/up (4096->11008), down (11008->4096) at B=2@0.803, "
+                    "B=16@0.638, B=64@0.520, each with its dense point (configs[2]); plus the down_proj B=16 "
+                    "sweep {0,0.25,0.5,0.638,0.8} (configs[1])")
+    else:
+        workload = "down_proj B=16 K=11008 N=4096 fp16, block sparsity sweep {0,0.25,0.5,0.638,0.8} (configs[1])"
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) stored [K,N], X~Laplace(0,0.05) (down) / N(0,1) "
+                "(others), masks rng.choice sorted; each point's graph rotates over >=1 GiB of distinct active "
+                "weight",
+        "config": {"workload": workload, "gemms_per_step": sum(p.copies for p in points),
+                   "value_is": "active-weight bytes / timed seconds over all points",
+                   "min_replay_GiB": round(min(p.replay_bytes for p in points) / 2**30, 3)},
+        "points": out_points,
+        "summary": {
+            "sparse_points": len(sparse),
+            "mean_frac_hbm_peak_sparse": round(statistics.mean(r["frac_hbm_peak"] for r in sparse), 4) if sparse else None,
+            "mean_speedup_over_ideal": round(statistics.mean(r["speedup_over_ideal"] for r in sparse), 4) if sparse else None,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
 
 
 def run_2d(args, dev):
     """2-D block sparsity (active output blocks as well as K-blocks): down_proj B=16 with half of the K-blocks
     active and a sweep of active 64-column output blocks, in place and compact.  Each point is
-    a graph of launches rotated over >= 1 GiB of weight copies; parity against the oracle
-    first.  Bytes per launch: na * 64 * (nn * 64) * 2 (active weight)."""
+    a graph of launches rotated over >= 1 GiB of distinct active weight; parity against the
+    oracle first.  Bytes per launch: na * 64 * (nn * 64) * 2 (active weight)."""
     import numpy as np
     import torch
 
-    import bsa_mi355x as bsa
     from bsa_mi355x import sparse2d
     from oracle import bsg_oracle as orc
 
     bt, k, n = 16, 11008, 4096
     nb_k, nb_n = orc.nblk_of(k), n // 64
-    x, w_kn, kidx = orc.make_inputs(1234, bt, k, n, "laplace", na=orc.n_active_for_sparsity(0.5, nb_k))
+    na = orc.n_active_for_sparsity(0.5, nb_k)
+    x, _, kidx = orc.make_inputs(SEED, bt, k, n, "laplace", na=na)
+    sweep = ((1.0, False), (0.75, False), (0.5, False), (0.25, False), (0.5, True))
+    min_nn = min(int(round(nd * nb_n)) for nd, _ in sweep)
+    pool = ShapePool("down", k, n, dev, copies_for(na * 64 * min_nn * 64 * 2))
     rng = np.random.default_rng(4321)
     xt, kt = torch.from_numpy(x).to(dev), torch.from_numpy(kidx).to(dev)
-    packed0 = bsa.pack_weight(torch.from_numpy(w_kn).to(dev), layout="kn")
-    copies = max(1, math.ceil(ROTATE_BYTES / packed0.numel() / 2))
-    packed = [packed0] + [packed0.clone() for _ in range(copies - 1)]
-    w_nk = np.ascontiguousarray(w_kn.T)
+    w_nk = np.ascontiguousarray(pool.w_kn_np.T)
     reps = max(5, args.steps)
     rows, total_bytes, total_us, focus = [], 0, 0.0, None
-    for nd, compact in ((1.0, False), (0.75, False), (0.5, False), (0.25, False), (0.5, True)):
+    for nd, compact in sweep:
         nn = int(round(nd * nb_n))
         nidx = np.sort(rng.choice(nb_n, nn, replace=False)).astype(np.int32)
         nt = torch.from_numpy(nidx).to(dev)
         y = torch.zeros(bt, nn * 64 if compact else n, dtype=torch.float16, device=dev)
         pl = sparse2d.plan_2d(bt, n, nn, nb_k, len(kidx), dev)
+        b = len(kidx) * 64 * nn * 64 * 2
+        copies = min(pool.copies, copies_for(b))
 
         def call(i, nt=nt, y=y, compact=compact, pl=pl):
-            return lambda: sparse2d.gemm_2d_packed(xt, packed[i % copies], n, kt, nt, y, compact=compact, plan=pl,
+            return lambda: sparse2d.gemm_2d_packed(xt, pool.packed[i], n, kt, nt, y, compact=compact, plan=pl,
                                                    workspace_prefix="bench2d")
 
         call(0)()
@@ -400,12 +604,12 @@ def run_2d(args, dev):
             raise SystemExit(f"2-D parity failure at n-density {nd} compact={compact}")
         med, mean = _graph_time([call(i) for i in range(copies)], reps)
         us, us_mean = med / copies, mean / copies
-        b = len(kidx) * 64 * nn * 64 * 2
         total_bytes += b * copies
         total_us += med
         name = f"down_b16_k500_n{int(round(nd * 1000)):04d}{'_compact' if compact else ''}"
         row = {"name": name, "active_k_blocks": len(kidx), "active_n_blocks": nn, "compact": compact,
-               "us_per_gemm": round(us, 3), "GBps_active": round(b / (us * 1e-6) / 1e9, 1), "plan": list(pl.as_tuple())}
+               "us_per_gemm": round(us, 3), "GBps_active": round(b / (us * 1e-6) / 1e9, 1),
+               "replay_GiB": round(b * copies / 2**30, 3), "plan": list(pl.as_tuple())}
         rows.append(row)
         log(json.dumps(row))
         if nd == 0.5 and not compact:
@@ -421,7 +625,7 @@ def run_2d(args, dev):
         "steps": reps, "warmup": 2, "ms_per_step": round(total_us / 1000.0, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: numpy PCG64 seed 1234 (X~Laplace(0,0.05), W~N(0,0.02)), K mask rng.choice of 86/172, "
-                "output-block masks rng.choice seed 4321; weights rotated over >=1 GiB of copies",
+                "output-block masks rng.choice seed 4321; each point rotates over >=1 GiB of distinct active weight",
         "config": {"workload": "2-D block sparsity: down_proj B=16 K=11008 N=4096, K density 0.5, output-block "
                                "density {1, 0.75, 0.5, 0.25} in place + 0.5 compact"},
         "points": rows,
@@ -435,7 +639,8 @@ def run_2d(args, dev):
 
 def run_fused(args, dev):
     """fused exact-L1 selection (k=31 of 64) + sparse GEMM on gate/up at B=64
-    (K=4096 -> N=11008), rotated over >= 1 GiB of weight copies; indices checked bit-exact."""
+    (K=4096 -> N=11008), rotated over >= 1 GiB of distinct active weight; indices checked
+    bit-exact against the oracle first."""
     import numpy as np
     import torch
 
@@ -443,32 +648,33 @@ def run_fused(args, dev):
     from bsa_mi355x.select import select_gemm_packed
     from oracle import bsg_oracle as orc
 
-    bt, k, n, keep = 64, 4096, 11008, 31
-    pt = Point("gate_up_b64_fused", bt, k, n, keep, "normal", 1234, dev)
+    bt, keep = 64, 31
+    k, n = SHAPES["gate_up"]
+    pool = ShapePool("gate_up", k, n, dev, copies_for(keep * 64 * n * 2))
+    pt = Point("gate_up_b64_fused", pool, bt, keep, dev)
     idx = torch.empty(keep, dtype=torch.int32, device=dev)
     cnt = torch.empty(1, dtype=torch.int32, device=dev)
-    select_gemm_packed(pt.x, pt.packed[0], n, keep, pt.y, idx_out=idx, count_out=cnt, workspace_prefix="fused_bench")
+    select_gemm_packed(pt.x, pool.packed[0], n, keep, pt.y, idx_out=idx, count_out=cnt, workspace_prefix="fused_bench")
     torch.cuda.synchronize()
     want = orc.select_topk_l1(pt.x_np, keep)
     got = idx.cpu().numpy()
     if not np.array_equal(got, want) or int(cnt.item()) != keep:
         raise SystemExit(f"fused selector indices differ from the oracle: {got} vs {want}")
-    y_ref = orc.gemm_ref(pt.x_np, np.ascontiguousarray(pt.w_kn_np.T), want)
+    y_ref = orc.gemm_ref(pt.x_np, np.ascontiguousarray(pool.w_kn_np.T), want)
     if not orc.within_tolerance(pt.y.float().cpu().numpy(), y_ref):
         raise SystemExit("fused select+GEMM output outside tolerance")
     log("fused: indices bit-exact, GEMM within tolerance")
     plan = bsa.resolve_plan(bt, n, pt.nblk, keep, dev)
-    ws_sel = "fused_sel"
 
     def fused(i):
-        return lambda: select_gemm_packed(pt.x, pt.packed[i], n, keep, pt.y, plan=plan, idx_out=idx, count_out=cnt,
+        return lambda: select_gemm_packed(pt.x, pool.packed[i], n, keep, pt.y, plan=plan, idx_out=idx, count_out=cnt,
                                           workspace_prefix="fused_bench")
 
     def gemm_only(i):
-        return lambda: bsa.gemm_packed(pt.x, pt.packed[i], n, idx, pt.y, plan=plan, workspace_prefix="fused_gemm")
+        return lambda: bsa.gemm_packed(pt.x, pool.packed[i], n, idx, pt.y, plan=plan, workspace_prefix="fused_gemm")
 
     def select_only(i):
-        return lambda: bsa.select_topk_l1(pt.x, keep, idx_out=idx, count_out=cnt, workspace_prefix=ws_sel)
+        return lambda: bsa.select_topk_l1(pt.x, keep, idx_out=idx, count_out=cnt, workspace_prefix="fused_sel")
 
     r = pt.copies
     reps = max(5, args.steps)
@@ -480,10 +686,12 @@ def run_fused(args, dev):
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": reps,
         "warmup": 2, "ms_per_step": round(t_fused * r / 1000.0, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) [K,N], X~N(0,1); weights rotated over >=1 GiB",
+        "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) [K,N], X~N(0,1); >=1 GiB of distinct active weight "
+                "per replay",
         "config": {"workload": "fused exact-L1 select (k=31 of 64) + sparse GEMM, gate/up B=64 K=4096 N=11008 "
-                               "(configs[3])", "plan": list(plan.as_tuple())},
+                               "(configs[3])", "plan": list(plan.as_tuple()), "launches_per_replay": r},
         "us_select_plus_gemm": round(t_fused, 3), "us_gemm_only": round(t_gemm, 3), "us_select_only": round(t_sel, 3),
+        "select_overhead_us": round(t_fused - t_gemm, 3),
         "indices_bit_exact": True,
     }
     print(json.dumps(line), flush=True)
@@ -492,7 +700,9 @@ def run_fused(args, dev):
 def run_decode(args, dev):
     """Llama-2-7B-shaped decode step of linears (layers x {qkv, o, gate/up,
     down}), B=64, per-projection masks from the fused selector at density 0.48 (k=31/64, 83/172),
-    the whole step captured as one hipGraph."""
+    the whole step captured as one hipGraph.  Its full parity check (every projection's indices,
+    first and last layer outputs, replay against eager) is tests/test_gpu_decode.py; here the
+    first and last layers are spot-checked before timing."""
     import numpy as np
     import torch
 
@@ -505,7 +715,6 @@ def run_decode(args, dev):
         f"{step.active_bytes / 1e9:.3f} GB active per step ({time.perf_counter() - t0:.1f} s to build)")
     step.capture()
     torch.cuda.synchronize()
-    # parity: first and last layer, every projection (indices bit-exact, outputs within tolerance)
     for li in sorted({0, args.layers - 1}):
         for p in step.layers[li]:
             x = p.x.cpu().numpy()
@@ -546,7 +755,7 @@ def run_decode(args, dev):
                                "{qkv N=12288, o, gate/up N=22016, down}, B=64, density 0.48, one hipGraph (configs[4])",
                    "resident_weight_gb": round(step.resident_weight_bytes / 1e9, 3),
                    "active_gb_per_step": round(step.active_bytes / 1e9, 4),
-                   "launches_per_step": 8 * args.layers},
+                   "launches_per_step": len(step.layers) * len(step.layers[0]) * 2},
         "step_ms_median": round(statistics.median(per), 4),
         "floor_ms_at_8TBps": round(step.active_bytes / 8e12 * 1e3, 4),
     }
@@ -554,30 +763,6 @@ def run_decode(args, dev):
 
 
 PERSTEP_FIXTURE = os.path.join(ROOT, "tests", "golden", "perstep_smaps.npz")
-PERSTEP_SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
-PERSTEP_PROJ_SHAPE = ["qkvo", "qkvo", "qkvo", "qkvo", "gate_up", "gate_up", "down"]
-
-
-class ShapePool:
-    """Packed-weight copies (>= 1 GiB) of one projection shape, plus [K,N] copies for
-    torch.mm, shared by every density and batch of the per-step replay."""
-
-    def __init__(self, name, k, n, dev, seed):
-        import numpy as np
-        import torch
-
-        import bsa_mi355x as bsa
-
-        self.name, self.k, self.n = name, k, n
-        self.nblk = (k + 63) // 64
-        rng = np.random.default_rng(seed)
-        w_kn = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float16)
-        self.w_kn_np = w_kn
-        w0 = torch.from_numpy(w_kn).to(dev)
-        p0 = bsa.pack_weight(w0, layout="kn")
-        self.copies = max(1, math.ceil(ROTATE_BYTES / (p0.numel() * 2)))
-        self.packed = [p0] + [p0.clone() for _ in range(self.copies - 1)]
-        self.w_kn = [w0] + [w0.clone() for _ in range(self.copies - 1)]
 
 
 def run_perstep(args, dev):
@@ -585,22 +770,32 @@ def run_perstep(args, dev):
     scripts/bench_perstep_actual_kernel_speedup.py): for each batch size, every group-step's
     S-map of 7 projections x 32 layers (tests/golden/perstep_smaps.npz, from the reference's
     results/oracle/perstep_batch_sweep.json) gives 224 GEMMs with density 1 - S and
-    floor(density * nblk) random active blocks (BPS:84-87).  Each distinct (shape, density) is
-    timed once (the reference's unique-case method, BPS:148-172) with this build's sparse kernel,
-    its dense variant and hipBLASLt (torch.mm), every one rotated over >= 1 GiB of weight
-    copies; a step's speedup is sum(dense) / sum(sparse) over its 224 GEMMs, averaged over the
-    55 group-steps of a batch size, next to the reference's A100X numbers for the same maps."""
+    floor(density * nblk) random active blocks (BPS:84-87), as bsa_mi355x.replay builds them.
+    Each distinct (shape, density) is timed once (the reference's unique-case method,
+    BPS:148-172) with this build's sparse kernel, its dense variant and hipBLASLt (torch.mm),
+    every one rotated over >= 1 GiB of distinct active weight; a step's speedup is
+    sum(dense) / sum(sparse) over its 224 GEMMs, averaged over the 55 group-steps of a batch
+    size, next to the reference's A100X numbers for the same maps."""
     import numpy as np
     import torch
 
     import bsa_mi355x as bsa
+    from bsa_mi355x import replay
     from oracle import bsg_oracle as orc
 
-    fx = np.load(PERSTEP_FIXTURE, allow_pickle=False)
+    fx = replay.load_maps(PERSTEP_FIXTURE)
     batches = [int(b) for b in (args.batches.split(",") if args.batches else fx["ref_batch"])]
-    pools = {name: ShapePool(name, k, n, dev, 1234 + i) for i, (name, (k, n)) in enumerate(PERSTEP_SHAPES.items())}
+    cases_by_b = replay.cases_for_batches(fx, batches)
+    need = {}
+    for cases in cases_by_b.values():
+        for name, tenths in cases:
+            k, n = replay.SHAPES[name]
+            na = replay.active_count(tenths, replay.nblk_of(name))
+            need[name] = max(need.get(name, 1), copies_for(na * 64 * n * 2))
+    pools = {name: ShapePool(name, k, n, dev, need.get(name, 1), seed=SEED + i)
+             for i, (name, (k, n)) in enumerate(replay.SHAPES.items())}
     log("perstep: weight pools " + ", ".join(f"{p.name} x{p.copies}" for p in pools.values()))
-    rng = np.random.default_rng(1234)
+    rng = np.random.default_rng(SEED)
     reps = max(3, min(args.steps, 10))
 
     def timed(fns):
@@ -610,51 +805,48 @@ def run_perstep(args, dev):
     total_bytes = 0.0
     total_us = 0.0
     for bt in batches:
-        sel = np.nonzero(fx["batch"] == bt)[0]
+        sel = replay.batch_rows(fx, bt)
         maps = fx["smap_tenths"][sel]  # [steps, 7, 32] sparsity in tenths
-        cases = sorted({(PERSTEP_PROJ_SHAPE[pi], 10 - int(t)) for m in maps for pi in range(7) for t in m[pi]})
+        cases = cases_by_b[bt]
         x = {name: torch.randn(bt, p.k, generator=torch.Generator().manual_seed(bt), dtype=torch.float32)
              .to(torch.float16).to(dev) for name, p in pools.items()}
         y = {name: torch.empty(bt, p.n, dtype=torch.float16, device=dev) for name, p in pools.items()}
         dense_us, mm_us = {}, {}
         for name, p in pools.items():
             pl = bsa.resolve_plan(bt, p.n, p.nblk, p.nblk, dev, None, dense=True)
+            nd = copies_for(p.packed_bytes)
             dense_us[name] = timed([(lambda i=i: bsa.gemm_packed(x[name], p.packed[i], p.n, None, y[name], plan=pl,
                                                                   workspace_prefix=f"ps_dense_{name}"))
-                                    for i in range(p.copies)])
-            mm_us[name] = timed([(lambda i=i: torch.mm(x[name], p.w_kn[i], out=y[name])) for i in range(p.copies)])
+                                    for i in range(nd)])
+            mm_us[name] = timed([(lambda w=w: torch.mm(x[name], w, out=y[name])) for w in p.w_kn(nd)])
         sparse_us = {}
         for name, tenths in cases:
             p = pools[name]
-            na = max(1, min(p.nblk, int(math.floor(tenths / 10.0 * p.nblk))))
-            idx = torch.from_numpy(np.sort(rng.choice(p.nblk, na, replace=False)).astype(np.int32)).to(dev)
+            na = replay.active_count(tenths, p.nblk)
+            idx = torch.from_numpy(replay.random_blocks(rng, p.nblk, na)).to(dev)
             pl = bsa.resolve_plan(bt, p.n, p.nblk, na, dev, None)
+            nc = min(p.copies, copies_for(na * 64 * p.n * 2))
             fns = [(lambda i=i: bsa.gemm_packed(x[name], p.packed[i], p.n, idx, y[name], plan=pl,
-                                                workspace_prefix=f"ps_{name}")) for i in range(p.copies)]
+                                                workspace_prefix=f"ps_{name}")) for i in range(nc)]
             fns[0]()
             torch.cuda.synchronize()
-            if tenths in (1, 5, 9):  # spot parity on three densities per shape
+            if tenths in (1, 5, 9):  # spot parity on three densities per shape (every case: tests/test_gpu_replay.py)
                 ref = orc.gemm_ref(x[name].float().cpu().numpy(), np.ascontiguousarray(p.w_kn_np.T),
                                    idx.cpu().numpy())
                 if not orc.within_tolerance(y[name].float().cpu().numpy(), ref):
                     raise SystemExit(f"perstep B={bt} {name} density {tenths / 10}: output outside tolerance")
             us = timed(fns)
-            sparse_us[(name, tenths)] = (us, na)
+            sparse_us[(name, tenths)] = us
             total_bytes += na * 64 * p.n * 2
             total_us += us
-        step_own, step_mm = [], []
+        step_own, step_mm, sparse_steps = [], [], []
         dense_total = sparse_total = 0.0
         for m in maps:
-            d_sum = m_sum = s_sum = 0.0
-            for pi in range(7):
-                name = PERSTEP_PROJ_SHAPE[pi]
-                for t in m[pi]:
-                    us, _ = sparse_us[(name, 10 - int(t))]
-                    s_sum += us
-                    d_sum += dense_us[name]
-                    m_sum += mm_us[name]
+            d_sum, s_sum = replay.step_sums(m, dense_us, sparse_us)
+            m_sum, _ = replay.step_sums(m, mm_us, sparse_us)
             step_own.append(d_sum / s_sum)
             step_mm.append(m_sum / s_sum)
+            sparse_steps.append(s_sum)
             dense_total += d_sum
             sparse_total += s_sum
         # Kernel replay throughput as scripts/analyze_perstep_kernel_replay_throughput.py:22-44 defines
@@ -671,8 +863,7 @@ def run_perstep(args, dev):
                                                      if ref_i is not None else None),
                "dense_us": {k: round(v, 2) for k, v in dense_us.items()},
                "hipblaslt_us": {k: round(v, 2) for k, v in mm_us.items()},
-               "sparse_us_step_mean": round(float(np.mean([sum(sparse_us[(PERSTEP_PROJ_SHAPE[pi], 10 - int(t))][0]
-                                                               for pi in range(7) for t in m[pi]) for m in maps])), 1),
+               "sparse_us_step_mean": round(float(np.mean(sparse_steps)), 1),
                "replay_tokens_per_s": {"dense": round(tokens / (dense_total * 1e-6), 1),
                                        "sparse": round(tokens / (sparse_total * 1e-6), 1),
                                        "throughput_speedup": round(dense_total / sparse_total, 3)},
@@ -686,7 +877,8 @@ def run_perstep(args, dev):
         "steps": reps, "warmup": 2, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16",
         "data": "reference S-maps (results/oracle/perstep_batch_sweep.json via tests/golden/perstep_smaps.npz); "
-                "W~N(0,0.02), X~N(0,1) synthetic; random masks floor(density*nblk); weights rotated over >=1 GiB",
+                "W~N(0,0.02), X~N(0,1) synthetic; random masks floor(density*nblk); each case rotates over >=1 GiB "
+                "of distinct active weight",
         "config": {"workload": "oracle-map replay of the 224-GEMM decode step (7 projections x 32 layers), "
                                "B in " + ",".join(map(str, batches)) + " (the reference's headline speedup table)",
                    "value_is": "active-weight bytes / time over every distinct timed sparse case"},
@@ -704,7 +896,6 @@ def main():
     import torch
 
     import bsa_mi355x as bsa
-    from oracle import bsg_oracle as orc
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -713,140 +904,16 @@ def main():
         return
     bsa.load()
     log(f"device {torch.cuda.get_device_name(dev)}; lib {bsa.load().bsg_version().decode()}")
-
-    if args.workload == "down_sweep":
-        k, n, bt = 11008, 4096, 16
-        points = []
-        for s in (0.0, 0.25, 0.5, 0.638, 0.8):
-            na = orc.n_active_for_sparsity(s, orc.nblk_of(k))
-            name = "down_b16_dense" if s == 0.0 else f"down_b16_s{int(round(s * 1000)):03d}"
-            points.append(Point(name, bt, k, n, na, "laplace", 1234, dev, dense=(s == 0.0)))
-            log(f"prepared {name}: na={na} copies={points[-1].copies} plan={points[-1].plan}")
-        workload = "down_proj B=16 K=11008 N=4096 fp16, block sparsity sweep {0,0.25,0.5,0.638,0.8} (configs[1])"
-        focus = "down_b16_s500"
-    elif args.workload == "llama":
-        shapes = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (11008, 4096)}
-        points = []
-        for bt, s in ((2, 0.803), (16, 0.638), (64, 0.520)):
-            for sh, (k, n) in shapes.items():
-                na = orc.n_active_for_sparsity(s, orc.nblk_of(k))
-                name = f"{sh}_b{bt}_s{int(round(s * 1000)):03d}"
-                points.append(Point(name, bt, k, n, na, "laplace" if sh == "down" else "normal", 1234, dev))
-                points.append(Point(f"{sh}_b{bt}_dense", bt, k, n, na, "laplace" if sh == "down" else "normal", 1234,
-                                    dev, dense=True))
-                log(f"prepared {name}: na={na} plan={points[-2].plan}")
-        workload = "Llama-2-7B q/k/v/o, gate/up, down at B=2@0.803, B=16@0.638, B=64@0.520 (configs[2])"
-        focus = "gate_up_b64_s520"
+    if args.workload in ("llama", "down_sweep"):
+        run_matrix(args, dev)
     elif args.workload == "fused":
         run_fused(args, dev)
-        return
     elif args.workload == "perstep":
         run_perstep(args, dev)
-        return
     elif args.workload == "2d":
         run_2d(args, dev)
-        return
     else:
         run_decode(args, dev)
-        return
-
-    if args.only:
-        points = [p for p in points if p.name == args.only]
-        if not points:
-            raise SystemExit(f"--only {args.only}: no such point")
-        focus = points[0].name
-    bad = []
-    for p in points:
-        rf, ok = p.check()
-        if not ok:
-            bad.append((p.name, rf))
-    if bad:
-        raise SystemExit(f"parity failure before timing: {bad}")
-    log("parity ok on every point")
-    for p in points:
-        p.capture()
-    step_graph = capture_step(points)
-    log("graphs captured")
-
-    total_ms, wall, per = time_points(points, step_graph, args.steps, args.warmup)
-    step_bytes = sum(p.active_bytes * p.copies for p in points)
-    value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
-    log(f"timed {args.steps} steps in {total_ms:.2f} ms (host wall {wall * 1e3:.1f} ms)")
-
-    dense_us = {}
-    for p in points:
-        if p.dense:
-            dense_us[p.name.replace("_dense", "")] = per[p.name][0]
-    out_points = []
-    for p in points:
-        med, mean = per[p.name]
-        gbs = p.active_bytes / (med * 1e-6) / 1e9
-        row = {"name": p.name, "B": p.bt, "K": p.k, "N": p.n, "active_blocks": p.nblk if p.dense else p.na,
-               "nblk": p.nblk, "us_per_gemm": round(med, 3), "GBps_active": round(gbs, 1),
-               "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-               "plan": list(p.plan.as_tuple())}
-        if p.bt >= 16:
-            row["mfma_util"] = round(p.flops / (med * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 5)
-        if not p.dense:
-            key = p.name.rsplit("_s", 1)[0] if args.workload == "llama" else "down_b16"
-            d = dense_us.get(key)
-            if d:
-                row["speedup_vs_dense"] = round(d / med, 3)
-                row["ideal_speedup"] = round(p.nblk / p.na, 3)
-                row["speedup_over_ideal"] = round((d / med) / (p.nblk / p.na), 3)
-        out_points.append(row)
-        log(json.dumps(row))
-
-    fp = next(p for p in points if p.name == focus)
-    f_med, f_mean = per[focus]
-    achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(focus),
-                "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
-                "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes}
-    if not args.only:
-        rd = read_calibration_us(fp)
-        roofline["practical_read"] = {
-            "us_per_launch": round(rd, 3), "GBps": round(fp.active_bytes / (rd * 1e-6) / 1e9, 1),
-            "frac_of_it": round(rd / f_mean, 4),
-            "what": "bsg_read_calibrate streaming the same bytes per launch (weight-load pattern, no compute), "
-                    "same rotation and timing"}
-        log(f"practical read of {fp.active_bytes / 1e6:.2f} MB: {rd:.2f} us ({roofline['practical_read']['GBps']} GB/s)")
-    dense_pt = next((p for p in points if p.dense and p.name.startswith("down_b16")), None)
-    if dense_pt is not None and not args.only:
-        mm = torch_mm_us(dense_pt)
-        for row in out_points:
-            if row["name"] == dense_pt.name:
-                row["torch_mm_us"] = round(mm, 3)
-        log(f"torch.mm (hipBLASLt) on {dense_pt.name}: {mm:.2f} us")
-    cpu = None
-    if not args.no_cpu and not args.only:
-        log("cpu baseline ...")
-        cpu = cpu_baseline(fp, args.cpu_seconds)
-        for p, row in zip(points, out_points):
-            row["cpu_us_per_gemm"] = round(cpu_point_us(p), 1)
-            row["gpu_speedup_over_cpu"] = round(row["cpu_us_per_gemm"] / row["us_per_gemm"], 1)
-    line = {
-        "metric": METRIC,
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(total_ms / args.steps, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) stored [K,N], X~Laplace(0,0.05)/N(0,1), "
-                "masks rng.choice sorted; weights rotated over >=1 GiB of copies",
-        "config": {"workload": workload, "gemms_per_step": sum(p.copies for p in points),
-                   "value_is": "active-weight bytes / timed seconds over all sweep points"},
-        "points": out_points,
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

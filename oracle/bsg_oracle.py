@@ -239,7 +239,8 @@ def select_scored_ref(x: np.ndarray, k: int, score: str = "l2_mean", prior=None,
                       eps: float = 0.1, scale=None, energy_keep: float = 0.0):
     """The reference's scoring rules (RRD:90-176) in float64, ranking by (score desc, id asc):
       score  = l2 (RRD:100) or energy [* scale] (RRD:103-105, 131), times
-               max(prior + eps, 1e-6)^alpha when a prior is given (RRD:106-112);
+               max(prior + eps, 1e-6)^alpha when a prior of exactly nblk entries is given
+               (RRD:106-112; a prior of any other length is ignored, as there);
       keep   = min(k, nblk), grown while energy_keep > 0 and the top-keep energy share is below
                it, to searchsorted(cum, energy_keep * total) + 1 clamped to [k, nblk] (RRD:165-176);
       ratio  = cumulative energy at keep / max(total, 1e-12) (RRD:141, 176).
@@ -247,8 +248,8 @@ def select_scored_ref(x: np.ndarray, k: int, score: str = "l2_mean", prior=None,
     l2, energy, es = block_stats64(x, scale)
     nb = len(energy)
     sc = (l2 if score == "l2_mean" else es).copy()
-    if prior is not None:
-        pr = np.asarray(prior, dtype=np.float64)[:nb] + float(eps)
+    if prior is not None and np.asarray(prior).size == nb:  # any other length is ignored (RRD:110-112)
+        pr = np.asarray(prior, dtype=np.float64).reshape(-1) + float(eps)
         sc = sc * np.maximum(pr, 1e-6) ** float(alpha)
     order = sorted(range(nb), key=lambda j: (-float(sc[j]), j))
     k0 = max(0, min(int(k), nb))
@@ -280,7 +281,7 @@ def select_scored_torch32(x, k: int, score: str = "l2_mean", prior=None, alpha: 
     else:
         sc = (xb.pow(2) * torch.as_tensor(np.asarray(scale, dtype=np.float32))[: total_k * BLOCK_K]
               .reshape(1, total_k, BLOCK_K)).sum(dim=2).mean(dim=0)
-    if prior is not None:
+    if prior is not None and int(np.asarray(prior).size) == int(total_k):  # RRD:110-112
         sc = sc * torch.clamp(torch.as_tensor(np.asarray(prior, dtype=np.float32)) + float(eps), min=1e-6).pow(
             float(alpha))
     k0 = max(0, min(int(k), total_k))
@@ -321,6 +322,15 @@ def make_inputs(seed: int, bt: int, k: int, n: int, x_dist: str = "laplace", na:
     nb = nblk_of(k)
     if na is None:
         na = nb
+    if isinstance(na, (list, tuple)):
+        # one mask per count, each drawn from the state right after X, so entry i equals the
+        # mask of make_inputs(seed, bt, k, n, x_dist, na[i])
+        state = rng.bit_generator.state
+        out = []
+        for m in na:
+            rng.bit_generator.state = state
+            out.append(np.sort(rng.choice(nb, size=int(m), replace=False)).astype(np.int32))
+        return x, w_kn, out
     idx = np.sort(rng.choice(nb, size=int(na), replace=False)).astype(np.int32)
     return x, w_kn, idx
 

@@ -211,3 +211,22 @@ def test_every_2d_tile(dev):
         got, want = ybv[:, written], ref_b[:, written]
         rf = orc.rel_frobenius(got, want)
         assert rf <= 5e-3 and np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want)), f"{what} bf16: {rf:.3e}"
+
+
+def test_2d_split_k_workspace_reuse_across_block_counts(dev):
+    """One cached workspace serves split-K 2-D launches with different active output-block
+    counts: the arrival counters sit at a fixed offset whatever a launch's tile count, so a
+    launch over many blocks after one over few (and a few-block launch again) is exact."""
+    bt, kdim, n = 16, 4096, 4096
+    x, w_nk, kb = case(64, bt, kdim, n, 40, "normal")
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    xt, kbt = to_dev(x, dev), to_dev(kb, dev)
+    plan = bsa.Plan(4, 16, 4, 4, 16, 1)  # split-K 4, 16-column work-groups: 4 tiles per output block
+    rng = np.random.default_rng(5)
+    for nn in (3, 20, 64, 3, 20):
+        nb = np.sort(rng.choice(64, nn, replace=False)).astype(np.int32)
+        y = torch.full((bt, n), SENTINEL, dtype=torch.float16, device=dev)
+        pl = s2d.gemm_2d_packed(xt, packed, n, kbt, to_dev(nb, dev), y, plan=plan, workspace_prefix="ws_reuse_2d")
+        assert pl.split_k == 4
+        torch.cuda.synchronize()
+        _check(y.float().cpu().numpy(), x, w_nk, kb, nb, False, f"workspace reuse nn={nn}")

@@ -1,0 +1,65 @@
+"""GPU parity of the per-step oracle-map replay (bench.py --workload perstep, the reference's
+headline benchmark scripts/bench_perstep_actual_kernel_speedup.py): for every batch size of the
+fixture, the first group-steps' maps give the distinct (shape, density) cases that bench.py times;
+each case runs through the same calls (tuned plan for (B, N, nblk, na), bsa.gemm_packed) and is
+checked against the oracle, as are the dense variants the speedups divide by."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import bsa_mi355x as bsa
+from bsa_mi355x import replay
+from helpers import assert_close
+from oracle import bsg_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "perstep_smaps.npz")
+STEPS_PER_BATCH = 2
+
+
+@pytest.fixture(scope="module")
+def weights(dev):
+    out = {}
+    for i, (name, (k, n)) in enumerate(replay.SHAPES.items()):
+        rng = np.random.default_rng(1234 + i)
+        w_kn = rng.normal(0.0, 0.02, size=(k, n)).astype(np.float16)
+        out[name] = (np.ascontiguousarray(w_kn.T), bsa.pack_weight(torch.from_numpy(w_kn).to(dev), layout="kn"))
+    yield out
+    out.clear()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("bt", [2, 4, 8, 16, 32, 64])
+def test_perstep_cases_match_oracle(dev, weights, bt):
+    fx = replay.load_maps(FIXTURE)
+    cases = replay.cases_for_batches(fx, [bt], steps_per_batch=STEPS_PER_BATCH)[bt]
+    assert cases, f"no group-step for B={bt}"
+    densities = {t for _, t in cases}
+    assert len(densities) >= 3, densities  # the maps span several densities
+    rng = np.random.default_rng(bt)
+    xs = {name: rng.normal(0, 1, size=(bt, k)).astype(np.float16) for name, (k, _) in replay.SHAPES.items()}
+    for name, (k, n) in replay.SHAPES.items():
+        w_nk, packed = weights[name]
+        nblk = replay.nblk_of(name)
+        xt = torch.from_numpy(xs[name]).to(dev)
+        y = torch.empty(bt, n, dtype=torch.float16, device=dev)
+        pl = bsa.resolve_plan(bt, n, nblk, nblk, dev, None, dense=True)
+        bsa.gemm_packed(xt, packed, n, None, y, plan=pl, workspace_prefix=f"rp_dense_{name}")
+        torch.cuda.synchronize()
+        assert_close(y.float().cpu().numpy(), orc.gemm_ref(xs[name], w_nk, np.arange(nblk)), f"B={bt} {name} dense")
+        for cname, tenths in cases:
+            if cname != name:
+                continue
+            na = replay.active_count(tenths, nblk)
+            idx = replay.random_blocks(rng, nblk, na)
+            pl = bsa.resolve_plan(bt, n, nblk, na, dev, None)
+            y.fill_(float("nan"))
+            bsa.gemm_packed(xt, packed, n, torch.from_numpy(idx).to(dev), y, plan=pl, workspace_prefix=f"rp_{name}")
+            torch.cuda.synchronize()
+            assert_close(y.float().cpu().numpy(), orc.gemm_ref(xs[name], w_nk, idx),
+                         f"B={bt} {name} density {tenths / 10} na={na} plan={pl.as_tuple()}")

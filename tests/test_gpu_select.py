@@ -221,3 +221,28 @@ def test_budget_selection_feeds_gemm_by_device_count(dev):
     want, keep, _ = orc.select_scored_ref(x, 8, "energy", energy_keep=0.6)
     assert c == keep and np.array_equal(idx[:c].cpu().numpy(), want)
     assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, want), "budget selection -> GEMM")
+
+
+def test_reference_drop_ins_ignore_a_prior_of_the_wrong_length(dev):
+    """The reference applies block_prior only when it has floor(K/64) entries and ignores it
+    otherwise (RRD:110-112, 135-138, 161-164): a shorter or longer prior gives the no-prior
+    result in all three drop-ins; the matching-length prior changes the selection; the library
+    entry point itself rejects a wrong length."""
+    rng = np.random.default_rng(12)
+    x = rng.laplace(0, 0.05, size=(16, 4096)).astype(np.float16)
+    x3 = to_dev(x, dev).view(16, 1, 4096)
+    base = bsa._select_active_blocks(x3, 0.3, 64).cpu().numpy()
+    r0 = bsa._topk_energy_ratio(x3, 0.3, 64)
+    e0, er0, ed0 = bsa._energy_expanded_active_blocks(x3, 0.2, 64, 0.5)
+    for length in (63, 65):
+        prior = torch.linspace(0.0, 3.0, length, device=dev)
+        assert np.array_equal(bsa._select_active_blocks(x3, 0.3, 64, block_prior=prior).cpu().numpy(), base)
+        assert bsa._topk_energy_ratio(x3, 0.3, 64, block_prior=prior) == r0
+        e, er, ed = bsa._energy_expanded_active_blocks(x3, 0.2, 64, 0.5, block_prior=prior)
+        assert np.array_equal(e.cpu().numpy(), e0.cpu().numpy()) and er == er0 and ed == ed0
+        with pytest.raises(ValueError):
+            bsa.select_topk(x3, 19, score="l2_mean", block_prior=prior)
+    prior = torch.linspace(0.0, 3.0, 64, device=dev)
+    got = bsa._select_active_blocks(x3, 0.3, 64, block_prior=prior).cpu().numpy()
+    want, _, _ = orc.select_scored_ref(x, orc.n_keep(0.3, 64), "l2_mean", prior=prior.cpu().numpy())
+    assert np.array_equal(got, want) and not np.array_equal(got, base)

@@ -170,3 +170,49 @@ def test_bench_traffic_profile_per_roofline_point():
         t = bench.load_traffic(point)
         assert isinstance(t, int) and algorithmic[point] <= t < 1.2 * algorithmic[point], (point, t)
     assert bench.load_traffic("qkvo_b2_s803") is None
+
+
+def _bench_module():
+    import importlib.util
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    return bench
+
+
+def test_bench_default_measures_configs2_with_active_byte_rotation():
+    """The default workload is BASELINE configs[2] (three projection shapes x B=2@0.803,
+    16@0.638, 64@0.520, each with a dense point) plus the configs[1] sweep, and every point's
+    graph reads >= 1 GiB of distinct ACTIVE weight (copies sized on active, not packed, bytes)."""
+    bench = _bench_module()
+    rows = bench.matrix_points("llama", None)
+    names = {r[0] for r in rows}
+    for sh in ("qkvo", "gate_up", "down"):
+        for b, s in ((2, "s803"), (16, "s638"), (64, "s520")):
+            assert f"{sh}_b{b}_{s}" in names and f"{sh}_b{b}_dense" in names
+    assert {"down_b16_s250", "down_b16_s500", "down_b16_s800"} <= names
+    assert dict((r[0], r[3]) for r in rows)["gate_up_b64_s520"] == 31
+    need = bench.pool_copies(rows)
+    for name, sh, bt, na, dense in rows:
+        k, n = bench.SHAPES[sh]
+        active = na * 64 * n * 2
+        copies = min(need[sh], bench.copies_for(active))
+        assert copies * active >= 1 << 30, (name, copies, active)
+    assert bench.KERNEL_NAMES[4] == "bsg_gemm_xl_kernel"
+
+
+def test_reference_prior_length_rule_on_the_host():
+    """The drop-in selectors pass a block prior on only when it holds floor(K/64) entries
+    (RRD:110-112): shorter and longer priors are dropped before any device call."""
+    import torch
+
+    from bsa_mi355x.select import _prior_or_none
+
+    x = torch.zeros(4, 1, 4096 + 32, dtype=torch.float16)  # floor(4128 / 64) = 64 scored blocks
+    for n in (63, 65, 1, 128):
+        assert _prior_or_none(torch.ones(n), x) is None
+    p = torch.ones(64)
+    assert _prior_or_none(p, x) is p
+    assert _prior_or_none(None, x) is None

@@ -222,6 +222,53 @@ def test_scored_selector_ties_and_prior():
     assert np.array_equal(ids, [1])  # prior clamped to 1e-6 for block 0; ties among 1..3 -> 1
 
 
+def test_prior_of_the_wrong_length_is_ignored():
+    """RRD:110-112 applies block_prior only when it holds exactly total_k entries: a shorter or
+    longer prior leaves the scores as without one, in both restatements."""
+    rng = np.random.default_rng(8)
+    x = rng.laplace(0, 0.05, size=(8, 4 * 64)).astype(np.float16)
+    base = orc.select_scored_ref(x, 2, "l2_mean")
+    base32 = orc.select_scored_torch32(x, 2, "l2_mean")
+    for prior in (np.array([0, 0, 9], np.float32), np.array([0, 0, 9, 9, 9], np.float32)):
+        got = orc.select_scored_ref(x, 2, "l2_mean", prior=prior)
+        got32 = orc.select_scored_torch32(x, 2, "l2_mean", prior=prior)
+        assert np.array_equal(got[0], base[0]) and np.array_equal(got32[0], base32[0])
+    ids, _, _ = orc.select_scored_ref(x, 2, "l2_mean", prior=np.array([0, 0, 9, 9], np.float32))
+    assert np.array_equal(ids, [2, 3])
+
+
+def test_make_inputs_several_masks_equal_single_draws():
+    """A list of counts gives, for each, the mask make_inputs draws for that count alone."""
+    x, w, masks = orc.make_inputs(77, 3, 640, 48, "laplace", na=[2, 5, 10])
+    for m, idx in zip((2, 5, 10), masks):
+        x1, w1, i1 = orc.make_inputs(77, 3, 640, 48, "laplace", na=m)
+        assert np.array_equal(x, x1) and np.array_equal(w, w1) and np.array_equal(idx, i1)
+
+
+def test_replay_case_bookkeeping():
+    """The per-step replay's cases follow BPS:84-87 and 124-135: density 1 - S clamped to
+    [0, 1], floor(density * nblk) blocks (at least one), one distinct case per (shape, density)."""
+    from bsa_mi355x import replay
+
+    assert replay.density_tenths(7) == 3 and replay.density_tenths(0) == 10 and replay.density_tenths(12) == 0
+    for nblk in (64, 172):
+        for s_tenths in range(11):  # the reference's float path: floor((1.0 - S) * nblk), S as stored
+            want = max(1, min(nblk, int(np.floor((1.0 - s_tenths / 10.0) * nblk))))
+            assert replay.active_count(replay.density_tenths(s_tenths), nblk) == want, (nblk, s_tenths)
+    assert replay.active_count(3, 64) == 19 and replay.active_count(5, 172) == 86 and replay.active_count(0, 64) == 1
+    m = np.zeros((7, 32), np.uint8)
+    m[6, :] = 8
+    m[0, 0] = 9
+    assert replay.unique_cases([m]) == [("down", 2), ("gate_up", 10), ("qkvo", 1), ("qkvo", 10)]
+    d, s = replay.step_sums(m, {"qkvo": 1.0, "gate_up": 2.0, "down": 3.0},
+                            {("down", 2): 0.5, ("gate_up", 10): 2.0, ("qkvo", 1): 0.1, ("qkvo", 10): 1.0})
+    assert d == 4 * 32 * 1.0 + 2 * 32 * 2.0 + 32 * 3.0
+    assert abs(s - (0.1 + 127 * 1.0 + 64 * 2.0 + 32 * 0.5)) < 1e-9
+    fx = replay.load_maps(os.path.join(os.path.dirname(__file__), "golden", "perstep_smaps.npz"))
+    cases = replay.cases_for_batches(fx, [2, 64], steps_per_batch=2)
+    assert set(cases) == {2, 64} and all(len(v) > 0 for v in cases.values())
+
+
 def test_perstep_fixture_matches_reference_summaries():
     """The S-map fixture (tests/golden/make_perstep_fixture.py, from the reference's result
     files) decodes to the mean sparsity the reference recorded for each group-step, and the

@@ -201,13 +201,14 @@ def ctypes_byref(p: Plan):
     return ctypes.byref(p)
 
 
-def _workspace(prefix: str, device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised workspace cached by (prefix, device, size) like the reference's
+def _workspace(prefix: str, device: torch.device, nbytes: int, layout: tuple = ()) -> torch.Tensor:
+    """Zero-initialised workspace cached by (prefix, device, size, layout) like the reference's
     split-K partial buffers (KRN:3099-3109).  The GEMM leaves its counters at zero, so a
-    cached workspace is reusable without clearing; two GEMMs in flight on different streams
-    must not share a prefix."""
+    cached workspace is reusable without clearing; `layout` (problem shape and plan) keeps
+    launches whose counter regions end at different offsets on separate buffers.  Two GEMMs in
+    flight on different streams must not share a prefix."""
     cache = _WORKSPACE_CACHE["bufs"]
-    key = (prefix, str(device), int(nbytes))
+    key = (prefix, str(device), int(nbytes), tuple(layout))
     buf = cache.get(key)
     if buf is None:
         _WORKSPACE_CACHE["misses"] += 1
@@ -332,7 +333,8 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
         na_for_plan = nblk
     pl = resolve_plan(bt, n_dim, nblk, na_for_plan, dev, plan, dense=(mode == "dense"))
     ws_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
-    ws_ptr = _workspace(workspace_prefix, dev, ws_bytes).data_ptr() if ws_bytes > 0 else None
+    ws_ptr = (_workspace(workspace_prefix, dev, ws_bytes, (bt, n_dim) + pl.as_tuple()).data_ptr()
+              if ws_bytes > 0 else None)
     kd = x2d.shape[1]
     with torch.cuda.device(dev):
         if mode == "list":

@@ -68,13 +68,21 @@ def _select_active_blocks_l1(x3: torch.Tensor, density: float, block_k: int = BL
 _SCORES = {"l1": _lib.BSG_SCORE_L1, "l2_mean": _lib.BSG_SCORE_L2_MEAN, "energy": _lib.BSG_SCORE_ENERGY}
 
 
-def _dev_f32(t: Optional[torch.Tensor], dev: torch.device, n: int, what: str) -> Optional[torch.Tensor]:
+def _dev_f32(t: Optional[torch.Tensor], dev: torch.device, n: int, what: str, exact: bool = False) -> Optional[torch.Tensor]:
     if t is None:
         return None
     t = t.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
-    if t.numel() < n:
+    if t.numel() < n or (exact and t.numel() != n):
         raise ValueError(f"{what} has {t.numel()} entries, needs {n}")
     return t
+
+
+def _prior_or_none(block_prior: Optional[torch.Tensor], x: torch.Tensor) -> Optional[torch.Tensor]:
+    """The reference applies a block prior only when it holds exactly floor(K/64) entries and
+    silently ignores it otherwise (RRD:110-112, 135-138, 161-164)."""
+    if block_prior is None or int(block_prior.numel()) != int(x.shape[-1]) // BLOCK_K:
+        return None
+    return block_prior
 
 
 def select_topk(x: torch.Tensor, k: int, score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
@@ -109,7 +117,7 @@ def select_topk(x: torch.Tensor, k: int, score: str = "l2_mean", block_prior: Op
     want_ratio = ratio_out is not None or (score != "l1" and energy_keep > 0)
     if want_ratio and ratio_out is None:
         ratio_out = torch.empty(1, dtype=torch.float32, device=dev)
-    prior = _dev_f32(block_prior, dev, nb, "block_prior")
+    prior = _dev_f32(block_prior, dev, nb, "block_prior", exact=True)
     scale = _dev_f32(channel_scale, dev, kd, "channel_scale")
     opts = _lib.SelectOpts(_SCORES[score], float(energy_keep), prior.data_ptr() if prior is not None else None,
                            float(prior_alpha), float(prior_eps), scale.data_ptr() if scale is not None else None,
@@ -135,7 +143,7 @@ def _select_active_blocks(x3: torch.Tensor, density: float, block_k: int = BLOCK
     nb = x3.shape[-1] // BLOCK_K
     nk = n_keep_for_density(density, nb)
     idx, _, _ = select_topk(x3, nk, score="energy" if block_score_scale is not None else "l2_mean",
-                            block_prior=block_prior, prior_alpha=prior_alpha, prior_eps=prior_eps,
+                            block_prior=_prior_or_none(block_prior, x3), prior_alpha=prior_alpha, prior_eps=prior_eps,
                             channel_scale=block_score_scale, workspace_prefix="select_ref")
     return idx[:nk]
 
@@ -154,8 +162,8 @@ def _topk_energy_ratio(x: torch.Tensor, density: float, block_k: int = BLOCK_K,
     nb = x3.shape[-1] // BLOCK_K
     nk = n_keep_for_density(density, nb)
     ratio = torch.empty(1, dtype=torch.float32, device=x3.device)
-    select_topk(x3, nk, score="energy", block_prior=block_prior, prior_alpha=prior_alpha, prior_eps=prior_eps,
-                ratio_out=ratio, workspace_prefix="select_ref")
+    select_topk(x3, nk, score="energy", block_prior=_prior_or_none(block_prior, x3), prior_alpha=prior_alpha,
+                prior_eps=prior_eps, ratio_out=ratio, workspace_prefix="select_ref")
     return float(ratio.item())
 
 
@@ -173,7 +181,8 @@ def _energy_expanded_active_blocks(x: torch.Tensor, density: float, block_k: int
         raise ValueError(f"block_k must be {BLOCK_K}")
     nb = x3.shape[-1] // BLOCK_K
     nk = n_keep_for_density(density, nb)
-    idx, cnt, ratio = select_topk(x3, nk, score="energy", block_prior=block_prior, prior_alpha=prior_alpha,
+    idx, cnt, ratio = select_topk(x3, nk, score="energy", block_prior=_prior_or_none(block_prior, x3),
+                                  prior_alpha=prior_alpha,
                                   prior_eps=prior_eps, energy_keep=float(energy_keep), workspace_prefix="select_ref")
     keep = int(cnt.item())
     return idx[:keep], float(ratio.item()), float(keep / nb)
@@ -214,7 +223,7 @@ def select_gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: i
     pl = resolve_plan(bt, n_dim, nblk, kk, dev, plan)
     sel_bytes = int(lib.bsg_select_workspace_bytes(m_dim))
     gemm_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
-    ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes)
+    ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes, (bt, n_dim) + pl.as_tuple())
     with torch.cuda.device(dev):
         check(lib.bsg_select_gemm(x2d.data_ptr(), x2d.stride(0), bt, m_dim, int(k), packed.data_ptr(), n_dim,
                                   idx_out.data_ptr(), count_out.data_ptr(), y2d.data_ptr(), y2d.stride(0),

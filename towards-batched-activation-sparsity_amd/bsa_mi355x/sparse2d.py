@@ -112,7 +112,8 @@ def gemm_2d_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_b
         ab, na = None, nblk
     pl = plan_2d(bt, int(n_dim), nn, nblk, na, dev, plan, dense=active_blocks is None)
     ws_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
-    ws_ptr = _workspace(workspace_prefix, dev, ws_bytes).data_ptr() if ws_bytes > 0 else None
+    ws_ptr = (_workspace(workspace_prefix, dev, ws_bytes, (bt, n_dim) + pl.as_tuple()).data_ptr()
+              if ws_bytes > 0 else None)
     with torch.cuda.device(dev):
         rc = lib.bsg_gemm_2d(x2d.data_ptr(), x2d.stride(0), bt, x2d.shape[1], packed.data_ptr(), n_dim,
                              ab.data_ptr() if ab is not None and na > 0 else None, na if ab is not None else 0,

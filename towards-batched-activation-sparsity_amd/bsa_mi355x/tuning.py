@@ -169,8 +169,16 @@ def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
     return out
 
 
+def _rotation(active_bytes: int, rotate_bytes: int) -> int:
+    """Launches per timing graph so that one replay reads >= rotate_bytes of distinct active weight."""
+    return max(1, math.ceil(rotate_bytes / max(1, int(active_bytes))))
+
+
 class _Case:
-    def __init__(self, bt: int, k: int, n: int, na: int, seed: int, device, rotate_bytes: int):
+    """One (shape, batch) under tuning: packed-weight copies for the smallest active-block count
+    that will be timed (min_na), inputs, and a block list set per density."""
+
+    def __init__(self, bt: int, k: int, n: int, na: int, seed: int, device, rotate_bytes: int, min_na: int = 0):
         import torch
 
         from .runtime import pack_weight
@@ -178,10 +186,11 @@ class _Case:
         g = torch.Generator(device="cpu").manual_seed(seed)
         self.bt, self.k, self.n, self.na = bt, k, n, na
         self.nblk = (k + BLOCK_K - 1) // BLOCK_K
+        self.rotate_bytes = rotate_bytes
         w = (torch.randn(k, n, generator=g) * 0.02).to(torch.float16).to(device)
         p0 = pack_weight(w, layout="kn")
         del w
-        copies = max(1, math.ceil(rotate_bytes / (p0.numel() * 2)))
+        copies = _rotation(max(1, min_na or na) * BLOCK_K * n * 2, rotate_bytes)
         self.packed = [p0] + [p0.clone() for _ in range(copies - 1)]
         self.x = torch.randn(bt, k, generator=g).to(torch.float16).to(device)
         perm = torch.randperm(self.nblk, generator=g)[: max(na, 0)]
@@ -189,13 +198,17 @@ class _Case:
         self.y = torch.empty(bt, n, dtype=torch.float16, device=device)
 
     def time(self, plan: Optional[Plan], dense: bool = False, reps: int = 5) -> float:
-        """Median µs per launch over `reps` graph replays of len(packed) rotated launches."""
+        """Median µs per launch over `reps` graph replays of R rotated launches, R copies holding
+        >= rotate_bytes of the blocks this launch reads (so the Infinity Cache serves no repeat)."""
         import torch
 
         from .runtime import gemm_packed
 
+        na = self.nblk if dense else int(self.idx.numel())
+        use = self.packed[: min(len(self.packed), _rotation(na * BLOCK_K * self.n * 2, self.rotate_bytes))]
+
         def run():
-            for p in self.packed:
+            for p in use:
                 gemm_packed(self.x, p, self.n, None if dense else self.idx, self.y, plan=plan,
                             workspace_prefix="tune")
 
@@ -218,7 +231,7 @@ class _Case:
             graph.replay()
             b.record()
             b.synchronize()
-            ts.append(a.elapsed_time(b) * 1000.0 / len(self.packed))
+            ts.append(a.elapsed_time(b) * 1000.0 / len(use))
         del graph
         return statistics.median(ts)
 
@@ -268,7 +281,8 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
     for sname, (k, n) in shapes.items():
         nblk = (k + BLOCK_K - 1) // BLOCK_K
         for bt in batch_sizes:
-            case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes)
+            min_na = min(max(1, min(nblk, int(math.floor(float(d) * nblk)))) for d in densities) if densities else nblk
+            case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes, min_na=min_na)
             dense_best = _pick(case, candidate_plans(bt, nblk, nblk), dense=True)
             entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": nblk, "dense": True,
                             "plan": list(dense_best[1].as_tuple()), "us": round(dense_best[0], 3)})

@@ -566,17 +566,27 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
   return BSG_OK;
 }
 
-int64_t gemm_ws_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
-  if (pl->split_k <= 1) return 0;
-  // enough for the 1-D tiling and for a 2-D launch over every 64-column block
+// Output tiles a split-K workspace is sized for: the 1-D tiling, or a 2-D launch over every
+// 64-column block, whichever is larger.  Every launch of a plan on (bt, N) keeps its arrival
+// counters in the first ws_counter_bytes and its partials right after, whatever its own tile
+// count (a 2-D launch over few output blocks uses a prefix of both), so calls that share a
+// workspace always agree on where the counters end.
+int64_t ws_max_tiles(int64_t bt, int64_t N, const bsg_plan* pl) {
   const int64_t gc = group_cols(pl);
   int64_t n_tiles = cdiv(cdiv(N, 16) * 16, gc);
   if (gc <= 64 && cdiv(N, 64) * (64 / gc) > n_tiles) n_tiles = cdiv(N, 64) * (64 / gc);
-  const int64_t tiles = n_tiles * cdiv(bt, pl->rows_per_group);
+  return n_tiles * cdiv(bt, pl->rows_per_group);
+}
+
+int64_t ws_counter_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
+  return cdiv(ws_max_tiles(bt, N, pl) * 4, 256) * 256;
+}
+
+int64_t gemm_ws_bytes(int64_t bt, int64_t N, const bsg_plan* pl) {
+  if (pl->split_k <= 1) return 0;
   const int64_t frag = (int64_t)(pl->rows_per_group / 16) * (group_cols(pl) / 16);
-  const int64_t part = tiles * pl->split_k * frag * 64 * 16;
-  const int64_t counters = cdiv(tiles * 4, 256) * 256;
-  return counters + part;
+  const int64_t part = ws_max_tiles(bt, N, pl) * pl->split_k * frag * 64 * 16;
+  return ws_counter_bytes(bt, N, pl) + part;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -687,10 +697,10 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.idx = idx;
   p.na_dev = na_dev;
   p.bitmap = bitmap;
-  const int64_t tiles = n_tiles * ygroups;
-  const int64_t cnt_bytes = cdiv(tiles * 4, 256) * 256;
+  if (n_tiles * ygroups > ws_max_tiles(bt, N, &pl))
+    return fail(BSG_ERR_UNSUPPORTED, "%lld output tiles exceed the workspace layout", (long long)(n_tiles * ygroups));
   p.cnt = need > 0 ? (uint32_t*)ws : nullptr;
-  p.part = need > 0 ? (float*)((char*)ws + cnt_bytes) : nullptr;
+  p.part = need > 0 ? (float*)((char*)ws + ws_counter_bytes(bt, N, &pl)) : nullptr;
   p.ldx = ldx;
   p.ldy = ldy;
   p.bt = (int32_t)bt;
