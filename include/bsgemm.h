@@ -225,6 +225,23 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
                     void* y, int64_t ldy, int dtype,
                     void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
+/* Allocation-free variant of bsg_select_gemm.  It has no counterpart in the reference: it is for
+ * callers that cannot allocate or hand over device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, selection, kernels and results
+ * as bsg_select_gemm, without the workspace: the selector's block scores and the GEMM's split-K
+ * counters and partials live in a library-owned static device array of
+ * BSG_NOALLOC_SCRATCH_BYTES on each GPU it runs on (held until the process ends).  Layout: 64 KiB
+ * of tile arrival counters, 16 KiB of block scores, the rest for partials.  A call whose plan
+ * needs more partials or counters than that returns BSG_ERR_WORKSPACE before any launch.  The
+ * first call on a device looks the array up and clears its counters (a kernel on `stream`).
+ * Nothing is allocated and no allocating library routine is called.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (concurrent streams, or host threads) race
+ * and must be serialised by the caller. */
+#define BSG_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int bsg_select_gemm_noalloc(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k,
+                            const void* wp, int64_t N, int32_t* idx_out, int32_t* na_out,
+                            void* y, int64_t ldy, int dtype, const bsg_plan* plan, void* stream);
+
 /* Read-rate calibration; no counterpart in the reference.  Streams `bytes` (a multiple of
  * 1024) from src with the GEMM's weight-load pattern (non-temporal 1 KiB wave loads, 8 waves
  * per compute unit) and writes sink[0] only if the data folds to a fixed constant.  Its

@@ -1,0 +1,106 @@
+"""The allocation-free select+GEMM entry point (bsg_select_gemm_noalloc) against the workspace
+entry point it mirrors (bsg_select_gemm), both called through the C ABI: the same selected
+blocks and count, and bit-identical outputs (the same kernels run on the same inputs), on two
+calls in a row whose second is smaller than the first (the static scratch keeps the first call's
+contents); a plan needing more partials than the scratch holds is rejected before any launch."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import bsa_mi355x as bsa
+from bsa_mi355x import _lib
+from helpers import assert_close, to_dev
+from oracle import bsg_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(dev, seed, bt, k, n):
+    x, w_kn, _ = orc.make_inputs(seed, bt, k, n, "laplace", na=1)
+    packed = bsa.pack_weight(to_dev(w_kn, dev), layout="kn")
+    return x, np.ascontiguousarray(w_kn.T), to_dev(x, dev), packed
+
+
+def _call(dev, fn_name, xt, packed, n, k, plan, ws=None):
+    lib = bsa.load()
+    bt, kd = xt.shape
+    nblk = (kd + 63) // 64
+    idx = torch.full((max(1, min(k, nblk)),), -1, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    y = torch.full((bt, n), float("nan"), dtype=torch.float16, device=dev)
+    pl = _lib.Plan(*plan)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if fn_name == "bsg_select_gemm":
+        rc = lib.bsg_select_gemm(xt.data_ptr(), kd, bt, kd, k, packed.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(),
+                                 y.data_ptr(), n, _lib.BSG_F16, ws.data_ptr(), ws.numel(), ctypes.byref(pl), stream)
+    else:
+        rc = lib.bsg_select_gemm_noalloc(xt.data_ptr(), kd, bt, kd, k, packed.data_ptr(), n, idx.data_ptr(),
+                                         cnt.data_ptr(), y.data_ptr(), n, _lib.BSG_F16, ctypes.byref(pl), stream)
+    assert rc == 0, (fn_name, rc, _lib.last_error())
+    torch.cuda.synchronize()
+    return idx, cnt, y
+
+
+def _workspace(dev, bt, k, n, keep, plan):
+    """The workspace bsg_select_gemm needs: the plan resolved as the library resolves it (kept
+    blocks, the device's compute units)."""
+    lib = bsa.load()
+    pl = _lib.Plan(*plan)
+    nblk = (k + 63) // 64
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert lib.bsg_plan_resolve(bt, n, nblk, min(keep, nblk), cu, ctypes.byref(pl)) == 0
+    nbytes = lib.bsg_select_workspace_bytes(k) + lib.bsg_gemm_workspace_bytes(bt, n, ctypes.byref(pl))
+    return torch.zeros(int(nbytes), dtype=torch.uint8, device=dev)
+
+
+# (bt, K, N, k, plan): split-K plans so the scratch's counters and partials are exercised; the
+# second of each pair is smaller (fewer rows, blocks and columns, or fewer tiles) than the first
+PAIRS = [
+    ((64, 11008, 4096, 83, (4, 16, 8, 4, 64, 4)), (16, 4096, 4096, 23, (2, 16, 2, 4, 16, 1))),
+    ((32, 4096, 11008, 31, (2, 16, 4, 4, 32, 2)), (8, 4096, 1024, 13, (2, 16, 2, 4, 16, 1))),
+    ((16, 11008, 4096, 62, (0, 0, 0, 0, 0, 0)), (2, 4096, 4096, 13, (0, 0, 0, 0, 0, 0))),
+]
+
+
+@pytest.mark.parametrize("first,second", PAIRS)
+def test_noalloc_matches_workspace_entry_point(dev, first, second):
+    for seed, (bt, k, n, keep, plan) in ((5, first), (6, second)):
+        x, w_nk, xt, packed = _inputs(dev, seed, bt, k, n)
+        i1, c1, y1 = _call(dev, "bsg_select_gemm_noalloc", xt, packed, n, keep, plan)
+        i0, c0, y0 = _call(dev, "bsg_select_gemm", xt, packed, n, keep, plan, ws=_workspace(dev, bt, k, n, keep, plan))
+        want = orc.select_topk_l1(x, keep)
+        assert int(c1.item()) == int(c0.item()) == len(want)
+        assert np.array_equal(i1.cpu().numpy()[: len(want)], want)
+        assert np.array_equal(i0.cpu().numpy()[: len(want)], want)
+        assert torch.equal(y1.view(torch.int16), y0.view(torch.int16)), (bt, k, n, plan)
+        assert_close(y1.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), f"noalloc bt={bt} K={k} N={n}")
+
+
+def test_noalloc_repeats_are_identical(dev):
+    """Back-to-back calls on one shape leave the scratch's counters re-armed: identical output."""
+    x, w_nk, xt, packed = _inputs(dev, 7, 64, 4096, 4096)
+    plan = (4, 16, 8, 4, 64, 4)
+    outs = [_call(dev, "bsg_select_gemm_noalloc", xt, packed, 4096, 31, plan)[2] for _ in range(3)]
+    for y in outs[1:]:
+        assert torch.equal(y.view(torch.int16), outs[0].view(torch.int16))
+
+
+def test_noalloc_rejects_a_plan_beyond_the_scratch(dev):
+    """Split-K partials beyond BSG_NOALLOC_SCRATCH_BYTES: BSG_ERR_WORKSPACE, nothing written."""
+    lib = bsa.load()
+    bt, k, n = 64, 4096, 22016
+    _, _, xt, packed = _inputs(dev, 8, bt, k, n)
+    idx = torch.full((31,), -1, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    y = torch.zeros(bt, n, dtype=torch.float16, device=dev)
+    pl = _lib.Plan(32, 16, 8, 4, 64, 4)  # 344 tiles x 32 splits x 16 KiB of partials: 176 MiB
+    rc = lib.bsg_select_gemm_noalloc(xt.data_ptr(), k, bt, k, 31, packed.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(),
+                                     y.data_ptr(), n, _lib.BSG_F16, ctypes.byref(pl),
+                                     torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == _lib.BSG_ERR_WORKSPACE and "static scratch" in _lib.last_error()
+    assert int(cnt.item()) == -1 and bool((idx == -1).all()) and not bool(y.any())

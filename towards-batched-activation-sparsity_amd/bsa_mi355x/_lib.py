@@ -26,6 +26,7 @@ BSG_F16 = 0
 BSG_BF16 = 1
 BLOCK_K = 64
 MAX_NBLK = 2048
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # BSG_NOALLOC_SCRATCH_BYTES
 
 
 class BsgError(RuntimeError):
@@ -122,6 +123,8 @@ SIGNATURES = {
                                _i64, _vp]),
     "bsg_select_gemm": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _i64,
                                _pplan, _vp]),
+    "bsg_select_gemm_noalloc": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int,
+                                       _pplan, _vp]),
     "bsg_read_calibrate": (_int, [_vp, _i64, _vp, _vp]),
 }
 

@@ -33,6 +33,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "bsg_device.hpp"
 #include "bsgemm.h"
 
@@ -637,6 +639,13 @@ struct LaunchExtras {
   int32_t nn = 0;
   const int32_t* nn_dev = nullptr;
   int ncompact = 0;
+  // Fixed split-K storage (the allocation-free entry point): counters and partials at these
+  // addresses, with room for cnt_cap_tiles counters and part_cap_bytes of partials, instead of
+  // being carved from ws.
+  uint32_t* cnt_fixed = nullptr;
+  float* part_fixed = nullptr;
+  int64_t cnt_cap_tiles = 0;
+  int64_t part_cap_bytes = 0;
 };
 
 int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp,
@@ -674,10 +683,21 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   rc = resolve(bt, ex.nidx != nullptr ? (int64_t)ex.nn * 64 : N, nblk, na, cu, &pl);
   if (rc != BSG_OK) return rc;
   const int64_t need = gemm_ws_bytes(bt, N, &pl);
-  if (need > 0 && !aligned16(ws)) return fail(BSG_ERR_ALIGN, "workspace must be 16-byte aligned");
-  if (need > 0 && (!ws || ws_bytes < need))
-    return fail(BSG_ERR_WORKSPACE, "workspace %lld bytes < %lld needed (split_k=%d)", (long long)ws_bytes,
-                (long long)need, pl.split_k);
+  const bool fixed_ws = ex.part_fixed != nullptr;
+  if (fixed_ws) {
+    const int64_t part_need = need > 0 ? need - ws_counter_bytes(bt, N, &pl) : 0;
+    if (need > 0 && (ws_max_tiles(bt, N, &pl) > ex.cnt_cap_tiles || part_need > ex.part_cap_bytes))
+      return fail(BSG_ERR_WORKSPACE,
+                  "split-K %d needs %lld tile counters and %lld bytes of partials; the static scratch holds "
+                  "%lld counters and %lld bytes (use the workspace entry point)",
+                  pl.split_k, (long long)ws_max_tiles(bt, N, &pl), (long long)part_need,
+                  (long long)ex.cnt_cap_tiles, (long long)ex.part_cap_bytes);
+  } else {
+    if (need > 0 && !aligned16(ws)) return fail(BSG_ERR_ALIGN, "workspace must be 16-byte aligned");
+    if (need > 0 && (!ws || ws_bytes < need))
+      return fail(BSG_ERR_WORKSPACE, "workspace %lld bytes < %lld needed (split_k=%d)", (long long)ws_bytes,
+                  (long long)need, pl.split_k);
+  }
   const KernelEntry* ke =
       find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
   const int64_t npad = cdiv(N, 16) * 16;
@@ -699,8 +719,8 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.bitmap = bitmap;
   if (n_tiles * ygroups > ws_max_tiles(bt, N, &pl))
     return fail(BSG_ERR_UNSUPPORTED, "%lld output tiles exceed the workspace layout", (long long)(n_tiles * ygroups));
-  p.cnt = need > 0 ? (uint32_t*)ws : nullptr;
-  p.part = need > 0 ? (float*)((char*)ws + ws_counter_bytes(bt, N, &pl)) : nullptr;
+  p.cnt = need > 0 ? (fixed_ws ? ex.cnt_fixed : (uint32_t*)ws) : nullptr;
+  p.part = need > 0 ? (fixed_ws ? ex.part_fixed : (float*)((char*)ws + ws_counter_bytes(bt, N, &pl))) : nullptr;
   p.ldx = ldx;
   p.ldy = ldy;
   p.bt = (int32_t)bt;
@@ -735,6 +755,47 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   hipLaunchKernelGGL(fn, grid, block, dyn_lds, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bsg_gemm launch");
+  return BSG_OK;
+}
+
+// The allocation-free entry point's storage: one static device array per GPU, laid out as
+// [tile arrival counters | exact-L1 block scores | split-K partials].  The counters start at
+// zero (the array is zero-filled when the code object loads, and cleared again on the first call
+// on each device) and every GEMM leaves them at zero; scores and partials are written before
+// they are read.  Host code never passes the array's name: it is a host-side stand-in, and a
+// kernel given it would fault.  Its device address comes from hipGetSymbolAddress, once per
+// device, and that address is what the kernels receive.
+constexpr int64_t kScratchCntBytes = 64 * 1024;                      // 16384 tile counters
+constexpr int64_t kScratchScoreBytes = BSG_MAX_NBLK * 8;             // uint64 scores, 16 KiB
+constexpr int64_t kScratchPartOff = kScratchCntBytes + kScratchScoreBytes;
+static_assert(kScratchPartOff % 256 == 0 && kScratchPartOff < BSG_NOALLOC_SCRATCH_BYTES, "scratch layout");
+
+static __device__ __attribute__((aligned(256))) unsigned char scratch[BSG_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[64] = {};
+
+// The scratch array's device address on the current device (looked up, and its counters
+// cleared on `stream`, on the first call there).
+int noalloc_scratch(char** out, void* stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= 64) return fail(BSG_ERR_UNSUPPORTED, "device ordinal %d (at most 63)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr || ((uintptr_t)ptr & 255u) != 0) return fail(BSG_ERR_HIP, "scratch address %p", ptr);
+    const int64_t n = kScratchCntBytes / 4;
+    hipLaunchKernelGGL(bsg_zero_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                       (uint32_t*)ptr, n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "scratch counter clear");
+    g_scratch_ptr[dev] = (char*)ptr;
+  }
+  *out = g_scratch_ptr[dev];
   return BSG_OK;
 }
 
@@ -869,9 +930,10 @@ int64_t bsg_select_workspace_bytes(int64_t K) {
   return cdiv(256 + cdiv(K, BSG_BLOCK_K) * 16, 256) * 256;
 }
 
-// Checks, then the score launch and (rank) the top-k launch of the exact-L1 selector.
-static int select_l1_launch(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
-                            int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream, bool rank) {
+// Checks, then the score launch (into scores[ceil(K/64)], 8-byte aligned) and (rank) the top-k
+// launch of the exact-L1 selector.
+static int select_l1_check(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const int32_t* idx_out,
+                           const int32_t* na_out, int dtype) {
   if (dtype != BSG_F16)
     return fail(BSG_ERR_DTYPE, "select: exact L1 scoring is defined for fp16 inputs (dtype=%d)", dtype);
   if (bt <= 0 || K <= 0) return fail(BSG_ERR_ARG, "select: bt=%lld K=%lld", (long long)bt, (long long)K);
@@ -882,14 +944,18 @@ static int select_l1_launch(const void* x, int64_t ldx, int64_t bt, int64_t K, i
   if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || !aligned16(x))
     return fail(BSG_ERR_ALIGN, "select: x must be 16-byte aligned, K %% 8 == 0, ldx %% 8 == 0");
   if (bt * 8 > 0x7fffffff) return fail(BSG_ERR_UNSUPPORTED, "select: bt too large");
-  const int64_t need = bsg_select_workspace_bytes(K);
-  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
-    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
-                (long long)need);
+  return BSG_OK;
+}
+
+static int select_l1_run(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
+                         int32_t* na_out, int dtype, uint64_t* scores, void* stream, bool rank) {
+  const int rc = select_l1_check(x, ldx, bt, K, k, idx_out, na_out, dtype);
+  if (rc != BSG_OK) return rc;
+  const int64_t nblk = cdiv(K, BSG_BLOCK_K);
   SelParams p;
   p.x = (const uint16_t*)x;
   p.ldx = ldx;
-  p.scores = (uint64_t*)((char*)ws + 256);
+  p.scores = scores;
   p.idx_out = idx_out;
   p.na_out = na_out;
   p.bt = (int32_t)bt;
@@ -904,6 +970,18 @@ static int select_l1_launch(const void* x, int64_t ldx, int64_t bt, int64_t K, i
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "bsg_select_topk_l1 rank launch");
   return BSG_OK;
+}
+
+// The exact-L1 selector with its scores in a caller workspace (after a 256-byte header).
+static int select_l1_launch(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
+                            int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream, bool rank) {
+  const int rc = select_l1_check(x, ldx, bt, K, k, idx_out, na_out, dtype);
+  if (rc != BSG_OK) return rc;
+  const int64_t need = bsg_select_workspace_bytes(K);
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
+                (long long)need);
+  return select_l1_run(x, ldx, bt, K, k, idx_out, na_out, dtype, (uint64_t*)((char*)ws + 256), stream, rank);
 }
 
 int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, int32_t* idx_out,
@@ -986,19 +1064,38 @@ int bsg_read_calibrate(const void* src, int64_t bytes, void* sink, void* stream)
   return BSG_OK;
 }
 
-int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp, int64_t N,
-                    int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
-                    const bsg_plan* plan, void* stream) {
-  const int64_t sel = bsg_select_workspace_bytes(K);
-  if (sel < 0) return fail(BSG_ERR_ARG, "select_gemm: K=%lld", (long long)K);
-  const int64_t nblk = cdiv(K, BSG_BLOCK_K);
+// The body of bsg_select_gemm and of its allocation-free variant: exact-L1 scores into
+// scores[ceil(K/64)], then the GEMM on the kept list, its split-K storage carved from
+// gws/gws_bytes or, when fx.part_fixed is set, taken from fx.  Every argument and the GEMM's
+// storage are checked before the first launch.
+static int select_gemm_run(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp,
+                           int64_t N, int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy, int dtype,
+                           uint64_t* scores, void* gws, int64_t gws_bytes, const LaunchExtras& fx,
+                           const bsg_plan* plan, void* stream) {
+  const int64_t nblk = K > 0 ? cdiv(K, BSG_BLOCK_K) : 0;
   if (k < 0) return fail(BSG_ERR_ARG, "select_gemm: k=%d", k);
-  if (bt <= 0 || N <= 0 || nblk > BSG_MAX_NBLK)
+  if (bt <= 0 || N <= 0 || K <= 0 || nblk > BSG_MAX_NBLK)
     return fail(BSG_ERR_ARG, "select_gemm: bt=%lld N=%lld K=%lld", (long long)bt, (long long)N, (long long)K);
+  int rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype, N);
+  if (rc != BSG_OK) return rc;
+  if (!idx_out || !na_out) return fail(BSG_ERR_ARG, "select_gemm: null idx_out or na_out");
   bsg_plan pl = plan ? *plan : bsg_plan{0, 0, 0, 0, 0, 0};
   const int32_t kk = k < nblk ? k : (int32_t)nblk;
-  int rc = resolve(bt, N, (int32_t)nblk, kk, pl.split_k == 0 ? device_cu_count() : 256, &pl);
+  rc = resolve(bt, N, (int32_t)nblk, kk, pl.split_k == 0 ? device_cu_count() : 256, &pl);
   if (rc != BSG_OK) return rc;
+  const int64_t need = gemm_ws_bytes(bt, N, &pl);
+  if (fx.part_fixed != nullptr) {
+    if (need > 0 && (ws_max_tiles(bt, N, &pl) > fx.cnt_cap_tiles ||
+                     need - ws_counter_bytes(bt, N, &pl) > fx.part_cap_bytes))
+      return fail(BSG_ERR_WORKSPACE,
+                  "select_gemm: split-K %d needs %lld tile counters and %lld bytes of partials; the static "
+                  "scratch holds %lld counters and %lld bytes",
+                  pl.split_k, (long long)ws_max_tiles(bt, N, &pl), (long long)(need - ws_counter_bytes(bt, N, &pl)),
+                  (long long)fx.cnt_cap_tiles, (long long)fx.part_cap_bytes);
+  } else if (need > 0 && (!gws || gws_bytes < need || !aligned16(gws))) {
+    return fail(BSG_ERR_WORKSPACE, "select_gemm: GEMM workspace %lld bytes < %lld needed (split_k=%d)",
+                (long long)gws_bytes, (long long)need, pl.split_k);
+  }
   // The GEMM ranks the scores itself when every work-group can do it quickly: the nblk^2
   // compares, in items of 64 blocks x 16 scores, come to at most 8 items per wave.  Otherwise a
   // one-work-group rank launch (about 3 us) is cheaper than ranking in each work-group.
@@ -1006,20 +1103,46 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
   if (nblk <= BSG_TOPK_MAX_NBLK && items <= 8 * (int64_t)pl.waves_per_group) {
     // Two launches: the block scores, then the GEMM, whose work-groups each rank them and walk
     // the kept list (work-group (0, 0) also publishes it).
-    rc = select_l1_launch(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream, false);
+    rc = select_l1_run(x, ldx, bt, K, k, idx_out, na_out, dtype, scores, stream, false);
     if (rc != BSG_OK) return rc;
-    const uint64_t* scores = (const uint64_t*)((const char*)ws + 256);
-    LaunchExtras ex;
+    LaunchExtras ex = fx;
     ex.scores = scores;
     ex.idx_out = idx_out;
     ex.na_out = na_out;
-    return launch_gemm(MODE_TOPK, x, ldx, bt, K, wp, N, nullptr, k, nullptr, nullptr, 0, y, ldy, dtype,
-                       (char*)ws + sel, ws_bytes - sel, &pl, stream, ex);
+    return launch_gemm(MODE_TOPK, x, ldx, bt, K, wp, N, nullptr, k, nullptr, nullptr, 0, y, ldy, dtype, gws,
+                       gws_bytes, &pl, stream, ex);
   }
-  rc = bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
+  rc = select_l1_run(x, ldx, bt, K, k, idx_out, na_out, dtype, scores, stream, true);
   if (rc != BSG_OK) return rc;
-  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, idx_out, kk, nullptr, nullptr, 0, y, ldy, dtype,
-                     (char*)ws + sel, ws_bytes - sel, &pl, stream);
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, idx_out, kk, nullptr, nullptr, 0, y, ldy, dtype, gws,
+                     gws_bytes, &pl, stream, fx);
+}
+
+int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp, int64_t N,
+                    int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy, int dtype, void* ws, int64_t ws_bytes,
+                    const bsg_plan* plan, void* stream) {
+  const int64_t sel = bsg_select_workspace_bytes(K);
+  if (sel < 0) return fail(BSG_ERR_ARG, "select_gemm: K=%lld", (long long)K);
+  if (!ws || ws_bytes < sel || ((uintptr_t)ws & 15u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select_gemm: workspace %lld bytes < the selector's %lld (16-byte aligned)",
+                (long long)ws_bytes, (long long)sel);
+  return select_gemm_run(x, ldx, bt, K, k, wp, N, idx_out, na_out, y, ldy, dtype, (uint64_t*)((char*)ws + 256),
+                         (char*)ws + sel, ws_bytes - sel, LaunchExtras{}, plan, stream);
+}
+
+int bsg_select_gemm_noalloc(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp,
+                            int64_t N, int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy, int dtype,
+                            const bsg_plan* plan, void* stream) {
+  char* base = nullptr;
+  int rc = noalloc_scratch(&base, stream);
+  if (rc != BSG_OK) return rc;
+  LaunchExtras fx;
+  fx.cnt_fixed = (uint32_t*)base;
+  fx.cnt_cap_tiles = kScratchCntBytes / 4;
+  fx.part_fixed = (float*)(base + kScratchPartOff);
+  fx.part_cap_bytes = BSG_NOALLOC_SCRATCH_BYTES - kScratchPartOff;
+  return select_gemm_run(x, ldx, bt, K, k, wp, N, idx_out, na_out, y, ldy, dtype,
+                         (uint64_t*)(base + kScratchCntBytes), nullptr, 0, fx, plan, stream);
 }
 
 }  // extern "C"
