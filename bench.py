@@ -54,7 +54,8 @@ TRAFFIC_PROFILES = {
     "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_xl_gate_up_b64_s520.md"),
 }
 # Kernel (symbol prefix) that each plan kind launches.
-KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel"}
+KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel",
+                5: "bsg_gemm_vt_kernel", 6: "bsg_gemm_vt_kernel"}
 
 
 def log(msg: str) -> None:
@@ -67,7 +68,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="llama",
-                    choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d"])
+                    choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d", "timeline"])
+    ap.add_argument("--plan", default=None, help="timeline workload: explicit plan a,b,c,d,e,f (default: tuned)")
     ap.add_argument("--batches", default=None, help="perstep workload: batch sizes (default: all six)")
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
@@ -887,8 +889,111 @@ def run_perstep(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def _pct(v, q):
+    v = sorted(v)
+    return v[min(len(v) - 1, max(0, int(round(q * (len(v) - 1)))))]
+
+
+def run_timeline(args, dev):
+    """Per-work-group phase timeline of one point (--only NAME of the llama workload), with the
+    profiling build of the library (libbsgemm_timeline.so: the same kernels, each work-group's wave
+    0 stamping the 100 MHz wall clock at its phase boundaries).  The point's R rotated launches are
+    captured as one graph (the bench's rotation) and replayed; the stamps of the last replay give,
+    per launch, each work-group's phases relative to the launch's first work-group start:
+    dispatch skew, list staging, first block consumed, main loop, epilogue, hand-off/end.  Also
+    reports the per-launch time of the graph, whose excess over the stamped span is the gap
+    between kernels."""
+    import numpy as np
+    import torch
+
+    import bsa_mi355x as bsa
+
+    lib = bsa.load()
+    if not args.only:
+        raise SystemExit("--workload timeline needs --only POINT")
+    khz = int(lib.bsg_timeline_clock_khz())
+    rows = [r for r in matrix_points("llama", dev) if r[0] == args.only]
+    if not rows:
+        raise SystemExit(f"--only {args.only}: no such point")
+    name, sh, bt, na, dense = rows[0]
+    pool = ShapePool(sh, *SHAPES[sh], dev, copies_for(na * 64 * SHAPES[sh][1] * 2))
+    plan = bsa.Plan(*[int(v) for v in args.plan.split(",")]) if args.plan else None
+    pt = Point(name, pool, bt, na, dev, dense=dense, plan=plan)
+    rf, ok = pt.check()
+    if not ok:
+        raise SystemExit(f"{name}: parity failure (rel_fro {rf})")
+    groups = 1 << 16
+    buf = torch.zeros(pt.copies * groups * 8, dtype=torch.int64, device=dev)
+    rc = lib.bsg_timeline_attach(buf.data_ptr(), pt.copies, groups)
+    if rc != 0:
+        raise SystemExit("the timeline workload needs BSA_MI355X_LIB=timeline (the profiling build): "
+                         + lib.bsg_last_error().decode())
+    pt.capture()
+    lib.bsg_timeline_attach(None, 0, 0)
+    reps = max(5, args.steps)
+    for _ in range(2):
+        pt.graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        pt.graph.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b) * 1000.0 / pt.copies)
+    per_launch = statistics.median(ts)
+    st = buf.view(pt.copies, groups, 8).cpu().numpy()
+    us = 1e3 / khz
+    phases = {"dispatch_skew": [], "list_staging": [], "first_block": [], "main_loop": [], "epilogue": [],
+              "handoff_end": [], "end_offset": []}
+    last = {"handoff_end": [], "end_offset": []}
+    spans, end_spread = [], []
+    n_groups = 0
+    for li in range(pt.copies):
+        g = st[li]
+        live = g[:, 5] > 0
+        g = g[live]
+        if len(g) == 0:
+            continue
+        n_groups = len(g)
+        t0 = g[:, 0].min()
+        spans.append((g[:, 5].max() - t0) * us)
+        end_spread.append((g[:, 5].max() - np.median(g[:, 5])) * us)
+        phases["dispatch_skew"] += list((g[:, 0] - t0) * us)
+        phases["list_staging"] += list((g[:, 1] - g[:, 0]) * us)
+        first = np.where(g[:, 2] > 0, g[:, 2], g[:, 3])
+        phases["first_block"] += list((first - g[:, 1]) * us)
+        phases["main_loop"] += list((g[:, 3] - first) * us)
+        phases["epilogue"] += list((g[:, 4] - g[:, 3]) * us)
+        phases["handoff_end"] += list((g[:, 5] - g[:, 4]) * us)
+        phases["end_offset"] += list((g[:, 5] - t0) * us)
+        ly = g[:, 6] == 1
+        last["handoff_end"] += list((g[ly, 5] - g[ly, 4]) * us)
+        last["end_offset"] += list((g[ly, 5] - t0) * us)
+    summary = {k: {"median": round(float(np.median(v)), 3), "p10": round(float(_pct(v, 0.1)), 3),
+                   "p90": round(float(_pct(v, 0.9)), 3)} for k, v in phases.items() if v}
+    summary_last = {k: {"median": round(float(np.median(v)), 3), "p90": round(float(_pct(v, 0.9)), 3)}
+                    for k, v in last.items() if v}
+    xcc = st[0, : n_groups, 7] >> 32
+    line = {"workload": "timeline", "point": name, "B": bt, "K": pt.k, "N": pt.n, "active_blocks": pt.na,
+            "plan": list(pt.plan.as_tuple()), "kernel": KERNEL_NAMES.get(pt.plan.kind), "launches": pt.copies,
+            "work_groups": int(n_groups), "clock_khz": khz,
+            "us_per_launch_graph": round(per_launch, 3),
+            "stamped_span_us": {"median": round(float(np.median(spans)), 3), "p90": round(float(_pct(spans, 0.9)), 3)},
+            "gap_between_kernels_us": round(per_launch - float(np.median(spans)), 3),
+            "end_spread_us": round(float(np.median(end_spread)), 3),
+            "phases_us": summary, "y_storing_groups_us": summary_last,
+            "groups_per_xcc": np.bincount(xcc.astype(np.int64), minlength=8).tolist()}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
+    if args.workload == "timeline":
+        # select the profiling build before the library is first loaded
+        os.environ["BSA_MI355X_LIB"] = "timeline"
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested); "
               "run with --gpus 1", file=sys.stderr)
@@ -912,6 +1017,8 @@ def main():
         run_perstep(args, dev)
     elif args.workload == "2d":
         run_2d(args, dev)
+    elif args.workload == "timeline":
+        run_timeline(args, dev)
     else:
         run_decode(args, dev)
 

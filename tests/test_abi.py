@@ -13,12 +13,15 @@ from bsa_mi355x import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "bsgemm.h")
+HEADERS = [HEADER, os.path.join(ROOT, "include", "bsgemm_timeline.h")]
 
 
 def _declared():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(bsg_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(bsg_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_and_library_exports_everything():
@@ -71,7 +74,12 @@ def test_plan_resolve_rejects():
     assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 7))[0] == _lib.BSG_ERR_UNSUPPORTED
+    # kind 5 (variable-width column groups): no split-K, only its instantiated widths
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(2, 48, 4, 4, 16, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(1, 80, 4, 4, 16, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
+    rc, p = _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 5))
+    assert rc == 0 and p.as_tuple() == (1, 48, 4, 4, 16, 5)
     # kind 4 pairs the waves over channel halves: one wave has no partner
     assert _resolve(64, 4096, 64, 1, plan=_lib.Plan(0, 16, 1, 4, 64, 4))[0] == _lib.BSG_ERR_UNSUPPORTED
     # kind 3: no split-K, 1-8 rows, and its activation staging must hold the list
@@ -220,3 +228,10 @@ def test_select_topk_rejects_bad_options():
     assert rc == _lib.BSG_ERR_ARG
     rc, msg = call(_lib.SelectOpts(_lib.BSG_SCORE_L2_MEAN, 0.0, None, 1.0, 0.1, None, None), k=-1)
     assert rc == _lib.BSG_ERR_ARG
+
+
+def test_shipped_library_has_no_timeline():
+    """The shipped build exports the profiling hook but rejects it (its kernels carry no stamps)."""
+    lib = bsa.load()
+    assert lib.bsg_timeline_attach(None, 0, 0) == 0
+    assert lib.bsg_timeline_attach(ctypes.c_void_p(0x1000), 1, 1) == _lib.BSG_ERR_UNSUPPORTED

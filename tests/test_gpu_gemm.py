@@ -125,7 +125,7 @@ def test_every_instantiated_tile(dev):
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     packed_b = bsa.pack_weight(wb.to(dev))
     for kind, rows, cols, waves, depth in tiles:
-        for sk in ((1,) if kind == 3 else (1, 3)):
+        for sk in ((1,) if kind in (3, 5, 6) else (1, 3)):
             # explicit plan through gemm_packed, so rows_per_group is honoured even when < bt
             out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
             p = bsa.Plan(sk, cols, waves, depth, rows, kind)
@@ -136,7 +136,7 @@ def test_every_instantiated_tile(dev):
         # bf16 once per tile (split-K 2)
         out_b = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
         bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b,
-                        plan=bsa.Plan(1 if kind == 3 else 2, cols, waves, depth, rows, kind),
+                        plan=bsa.Plan(1 if kind in (3, 5, 6) else 2, cols, waves, depth, rows, kind),
                         workspace_prefix="tiles_bf")
         torch.cuda.synchronize()
         yb = out_b.float().cpu().numpy()
@@ -362,3 +362,40 @@ def test_strided_rows_and_side_stream(dev, plan):
     y = y_wide.float().cpu().numpy()
     assert np.all(y[:, n:] == 7.0), "columns past N were written"
     assert_close(y[:, :n], orc.gemm_ref64(x, w_nk, idx), f"strided {plan}")
+
+
+@pytest.mark.parametrize("bt,k,n,na", [(64, 4096, 11008, 31), (37, 4096, 11008, 23), (16, 4096, 11008, 23),
+                                       (2, 4096, 11008, 13), (64, 11008, 4096, 83), (33, 4096, 12288, 31),
+                                       (16, 4096, 22016, 31), (5, 1000, 1000, 7)])
+def test_variable_width_column_groups(dev, bt, k, n, na):
+    """Kinds 5 and 6 deal N/16 subtiles to the work-groups as evenly as possible (2 or 3 each at
+    N=11008 on 256 compute units, 1-6 elsewhere): every subtile written exactly once, list, dense
+    and bitmap modes, against the oracle; repeated launches are bit-identical."""
+    x, w_nk, idx = case(77 + bt, bt, k, n, na, "normal")
+    xt, it = to_dev(x, dev), to_dev(idx, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    ref = orc.gemm_ref64(x, w_nk, idx)
+    rows = 16 if bt <= 16 else (32 if bt <= 32 else 64)
+    k6 = {16: ((6, 48, 2, 4), (6, 48, 4, 4)), 32: ((6, 48, 2, 4), (6, 48, 4, 2)), 64: ((6, 48, 2, 2), (6, 48, 4, 2))}
+    for kind, cols, waves, depth in ((5, 48, 4, 4), (5, 32, 2, 4), (5, 96, 2, 4), (5, 16, 4, 4)) + k6[rows]:
+        p = bsa.Plan(1, cols, waves, depth, rows, kind)
+        out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        print(f"kind {kind} bt={bt} K={k} N={n} plan={p.as_tuple()}", flush=True)
+        used = bsa.gemm_packed(xt, packed, n, it, out, plan=p, workspace_prefix="vt")
+        assert used.as_tuple() == p.as_tuple(), used
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), ref, f"kind {kind} {p.as_tuple()} bt={bt} N={n}")
+        again = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        bsa.gemm_packed(xt, packed, n, it, again, plan=p, workspace_prefix="vt")
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    p = bsa.Plan(1, 48, 4, 4, rows, 5)
+    dense = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+    bsa.gemm_packed(xt, packed, n, None, dense, plan=p, workspace_prefix="vt")
+    bm = torch.zeros(orc.nblk_of(k), dtype=torch.uint8, device=dev)
+    bm[it.long()] = 1
+    bout = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+    bsa.gemm_packed(xt, packed, n, None, bout, bitmap=bm, plan=p, workspace_prefix="vt")
+    torch.cuda.synchronize()
+    assert_close(dense.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.arange(orc.nblk_of(k))), "kind 5 dense")
+    assert_close(bout.float().cpu().numpy(), ref, "kind 5 bitmap")

@@ -12,7 +12,10 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libbsgemm.so")
+# BSA_MI355X_LIB=timeline selects the phase-timeline profiling build (libbsgemm_timeline.so,
+# same ABI, kernels that record per-work-group stamps); the default is the shipped library.
+LIB_PATH = os.path.join(_HERE, "libbsgemm_timeline.so" if os.environ.get("BSA_MI355X_LIB") == "timeline"
+                        else "libbsgemm.so")
 
 BSG_OK = 0
 BSG_ERR_ARG = -1
@@ -126,6 +129,9 @@ SIGNATURES = {
     "bsg_select_gemm_noalloc": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int,
                                        _pplan, _vp]),
     "bsg_read_calibrate": (_int, [_vp, _i64, _vp, _vp]),
+    # include/bsgemm_timeline.h
+    "bsg_timeline_attach": (_int, [_vp, _i64, _i64]),
+    "bsg_timeline_clock_khz": (_i64, []),
 }
 
 _lock = threading.Lock()

@@ -157,6 +157,10 @@ def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
             if rows == fma_rows:
                 out.append(Plan(1, cols, waves, depth, rows, kind))
             continue
+        if kind >= 5:  # variable-width column groups: the chip is filled without split-K
+            if rows == rb:
+                out.append(Plan(1, cols, waves, depth, rows, kind))
+            continue
         # 32-row batches also try 64-row tiles; 32- and 64-row batches also try two row groups of
         # half the rows, which read each weight block twice, concurrently, but fill the chip
         # without split-K
@@ -322,6 +326,54 @@ def tune(shapes: Dict[str, Tuple[int, int]], batch_sizes: Sequence[int], densiti
     return entries
 
 
+def refine(shapes: Sequence[str], batch_sizes: Sequence[int], kinds: Sequence[int] = (5, 6),
+           table: str = TABLE_PATH, out_table: Optional[str] = None, rotate_bytes: int = 1 << 30, seed: int = 1234,
+           margin: float = 0.03, log=print) -> List[dict]:
+    """Re-time the shipped table's entries for the given shapes and batches against the candidate
+    plans of `kinds` (the kernels added after the table was made), keeping a new plan only when it
+    beats the shipped one by more than `margin` on the same case (both timed in one run)."""
+    import torch
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    with open(table) as f:
+        data = json.load(f)
+    entries = data["entries"]
+    t_start = time.time()
+    for sname in shapes:
+        k, n = LLAMA2_7B_SHAPES[sname]
+        nblk = (k + BLOCK_K - 1) // BLOCK_K
+        for bt in batch_sizes:
+            rows = [e for e in entries if e["shape"] == sname and int(e["bt"]) == bt]
+            if not rows:
+                continue
+            min_na = min(int(e["na"]) for e in rows)
+            case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes, min_na=min_na)
+            gen = torch.Generator().manual_seed(seed)
+            for e in sorted(rows, key=lambda e: (not e["dense"], int(e["na"]))):
+                na = int(e["na"])
+                dense = bool(e["dense"])
+                case.idx = torch.randperm(nblk, generator=gen)[:na].sort()[0].to(torch.int32).to(dev)
+                old = Plan(*e["plan"])
+                cands = [p for p in candidate_plans(bt, na, nblk) if p.kind in kinds]
+                best_us, best = _pick(case, [old] + cands, dense=dense)
+                old_us = statistics.median([case.time(old, dense=dense) for _ in range(3)])
+                new_us = statistics.median([case.time(best, dense=dense) for _ in range(3)]) if best else float("inf")
+                if best is not None and best.as_tuple() != old.as_tuple() and new_us < old_us * (1.0 - margin):
+                    e["plan"], e["us"] = list(best.as_tuple()), round(new_us, 3)
+                    verdict = "replaced"
+                else:
+                    e["us"] = round(old_us, 3)
+                    verdict = "kept"
+                log(f"[refine {time.time() - t_start:6.1f}s] {sname} B={bt} na={na}{' dense' if dense else ''}: "
+                    f"{verdict} {old.as_tuple()} {old_us:.2f} us vs {best.as_tuple() if best else None} {new_us:.2f} us")
+            del case
+            torch.cuda.empty_cache()
+    with open(out_table or table, "w") as f:
+        json.dump(data, f, indent=1)
+    load_table(out_table or table)
+    return entries
+
+
 def main(argv: Optional[Iterable[str]] = None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shapes", default="qkvo,gate_up,down")
@@ -331,7 +383,15 @@ def main(argv: Optional[Iterable[str]] = None) -> None:
     ap.add_argument("--lookup-dir", default=None)
     ap.add_argument("--merge", action="store_true",
                     help="keep the other (shape, batch) entries of the shipped table in the output")
+    ap.add_argument("--refine-kinds", default=None,
+                    help="instead of a full search, re-time the shipped entries against these kinds (e.g. 5,6)")
+    ap.add_argument("--table", default=TABLE_PATH, help="--refine-kinds: the table to start from")
     args = ap.parse_args(list(argv) if argv is not None else None)
+    if args.refine_kinds:
+        refine(args.shapes.split(","), [int(b) for b in args.batch_sizes.split(",")],
+               kinds=[int(v) for v in args.refine_kinds.split(",")], table=args.table, out_table=args.out,
+               log=lambda m: print(m, flush=True))
+        return
     shapes = {s: LLAMA2_7B_SHAPES[s] for s in args.shapes.split(",")}
     tune(shapes, [int(b) for b in args.batch_sizes.split(",")], [float(d) for d in args.densities.split(",")],
          out_table=args.out, lookup_dir=args.lookup_dir, log=lambda m: print(m, flush=True),

@@ -20,10 +20,13 @@ CSRC = os.path.join(PKG_ROOT, "csrc")
 # The C ABI and host code, then the tile tables (each instantiates a slice of the kernel
 # templates of bsg_device.hpp); the units compile in parallel and link into one library.
 SOURCES = ["bsgemm.hip", "tiles_k1_r16.hip", "tiles_k1_r32.hip", "tiles_k1_r64.hip", "tiles_k2.hip",
-           "tiles_k4.hip", "tiles_k3.hip"]
+           "tiles_k4.hip", "tiles_k3.hip", "tiles_k5.hip"]
 SRC = os.path.join(CSRC, "bsgemm.hip")
 INCLUDE = os.path.join(REPO_ROOT, "include")
 OUT = os.path.join(PKG_ROOT, "bsa_mi355x", "libbsgemm.so")
+# The phase-timeline profiling build: the same sources with -DBSG_TIMELINE (per-work-group
+# wall-clock stamps, include/bsgemm_timeline.h); selected at run time by BSA_MI355X_LIB=timeline.
+OUT_TIMELINE = os.path.join(PKG_ROOT, "bsa_mi355x", "libbsgemm_timeline.so")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -55,22 +58,25 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, jobs: int = 0) -> str:
-    """Compile libbsgemm.so (always recompiles every unit) and return its path."""
+def build(verbose: bool = False, jobs: int = 0, timeline: bool = False) -> str:
+    """Compile libbsgemm.so, or with timeline=True libbsgemm_timeline.so (always recompiles every
+    unit), and return its path."""
     cc = hipcc()
     jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
+    out = OUT_TIMELINE if timeline else OUT
+    extra = ["-DBSG_TIMELINE"] if timeline else []
     with tempfile.TemporaryDirectory(prefix="bsgemm_build_") as tmpdir:
         objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-        cmds = [[cc, *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, s), "-o", o]
+        cmds = [[cc, *HIPCC_FLAGS, *extra, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, s), "-o", o]
                 for s, o in zip(SOURCES, objs)]
         with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
             for f in [pool.submit(_run, c, verbose) for c in cmds]:
                 f.result()
-        tmp = OUT + ".tmp"
+        tmp = out + ".tmp"
         _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, timeline="--timeline" in sys.argv[1:]))

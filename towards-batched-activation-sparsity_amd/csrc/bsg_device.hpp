@@ -36,11 +36,14 @@ struct GemmParams {
   const int32_t* nidx;
   const int32_t* nn_dev;
   int32_t nn, ncompact, ny;
+  // Phase timeline of a profiling build (-DBSG_TIMELINE): 8 stamps per work-group, or null.  The
+  // shipped build never reads it.
+  uint64_t* tl;
 };
 
 typedef void (*GemmFn)(GemmParams);
 
-enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4 };
+enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4, KIND_VT = 5, KIND_VT1 = 6 };
 
 // 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
 struct KernelEntry {
@@ -54,7 +57,7 @@ struct TileTable {
   int n;
 };
 
-extern const TileTable kTilesK1R16, kTilesK1R32, kTilesK1R64, kTilesK2, kTilesK4, kTilesK3;
+extern const TileTable kTilesK1R16, kTilesK1R32, kTilesK1R64, kTilesK2, kTilesK4, kTilesK3, kTilesK5;
 
 }  // namespace bsgk
 
@@ -72,6 +75,36 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kOOB = (int)0x80000000u;  // buffer offset beyond any num_records we build
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+// Phase timeline (a separate profiling build of the library, compiled with -DBSG_TIMELINE; in
+// the shipped build these expand to nothing).  Wave 0 of each work-group keeps the 100 MHz wall
+// clock at its phase boundaries in registers and writes them once at the end to
+// p.tl[group * 8 + slot]: 0 entry, 1 block list staged, 2 first block's weights consumed,
+// 3 main loop done, 4 outputs or partials issued, 5 end (own stores acknowledged),
+// 6 = 1 when this work-group stored Y (the last arriver under split-K), 7 = XCC id << 32 | HW_ID.
+#ifdef BSG_TIMELINE
+#define BSG_TL_DECL uint64_t bsg_ts_[6] = {0, 0, 0, 0, 0, 0};
+#define BSG_TL(i) (bsg_ts_[i] = wall_clock64())
+#define BSG_TL_IF(i, cond) \
+  if (cond) bsg_ts_[i] = wall_clock64()
+#define BSG_TL_END(p, stored_y)                                                                         \
+  do {                                                                                                 \
+    __builtin_amdgcn_s_waitcnt(0x0F70);                                                                \
+    bsg_ts_[5] = wall_clock64();                                                                       \
+    if ((p).tl != nullptr && threadIdx.x == 0) {                                                       \
+      uint64_t* t_ = (p).tl + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;                      \
+      for (int i_ = 0; i_ < 6; ++i_) t_[i_] = bsg_ts_[i_];                                             \
+      t_[6] = (stored_y) ? 1u : 0u;                                                                    \
+      t_[7] = ((uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |                          \
+              (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);                                     \
+    }                                                                                                  \
+  } while (0)
+#else
+#define BSG_TL_DECL
+#define BSG_TL(i) ((void)0)
+#define BSG_TL_IF(i, cond) ((void)0)
+#define BSG_TL_END(p, stored_y) ((void)0)
+#endif
 
 enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2, MODE_TOPK = 3 };
 // A GEMM ranks block scores itself (MODE_TOPK) up to this many blocks: keys and ranks fit its
@@ -519,8 +552,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   int n0, n0y;
   if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
   const int y0 = blockIdx.y * (16 * BTT);
+  BSG_TL_DECL
+  BSG_TL(0);
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  BSG_TL(1);
 
   // This wave's contiguous slice [pbeg, pend) of the list.
   const int G = S * WPG;
@@ -591,9 +627,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       compute(wv[d], xv[d]);
+      BSG_TL_IF(2, t0 == 0 && d == 0);
       issue(wv[d], xv[d], t0 + d + DEPTH);
     }
   }
+  BSG_TL(3);
 
   const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
   auto emit = [&](int f, f32x4 v) {
@@ -630,7 +668,9 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       for (int s = 0; s < NSUB; ++s) emit(bi * NSUB + s, acc[bi][s]);
   }
 
+  BSG_TL(4);
   if (S > 1) splitk_finish<T, BTT, NSUB, NSUB, F>(p, tile_lin, y0, n0y, sk, 0, w == 0, acc, &s_misc[WPG]);
+  BSG_TL_END(p, S == 1 || s_misc[WPG] != 0);
 }
 
 // Kinds 2 and 4 ("xlds"): one work-group = BTT*16 batch rows x WC*NSUB*16 columns; its waves
@@ -665,8 +705,11 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   int n0, n0y;
   if (!tile_columns<N2D>(p, tile, 16 * CS, &n0, &n0y)) return;
   const int y0 = blockIdx.y * (16 * BTT);
+  BSG_TL_DECL
+  BSG_TL(0);
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  BSG_TL(1);
 
   // The work-group's contiguous slice of the list (all its waves walk it together).
   const int pbeg = (int)(((int64_t)na * sk) / S);
@@ -739,9 +782,11 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
           for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xb, acc[bi][s]);
         }
       }
+      BSG_TL_IF(2, t0 == 0 && d == 0);
       issue(wv[d], xs[d], t0 + d + DEPTH);
     }
   }
+  BSG_TL(3);
 
   if constexpr (WK > 1) {
     // The second channel half hands its accumulators to the first through LDS.
@@ -773,14 +818,17 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
           part_emit<FT>(p, tile_lin, sk, g, acc[bi][s]);
       }
   }
+  BSG_TL(4);
   if (S > 1) splitk_finish<T, BTT, NSUB, CS, FT>(p, tile_lin, y0, n0y, sk, wc, wk == 0, acc, &s_misc[WPG]);
+  BSG_TL_END(p, S == 1 || s_misc[WPG] != 0);
 }
 
 // Kind 3 ("fma", batch tiles of 1-8 rows): the contraction is too thin for MFMA, so each lane
 // multiplies the 8 consecutive channels of one weight column that its 16-byte load of the packed
-// tile holds (channels 32h + 8g .. +7 of column c, g = lane / 16, c = lane % 16) with the same
-// channels of every batch row, in fp32 with packed fp16/bf16 dot products, and the four lanes
-// of a column (g = 0..3) are summed once at the end.  The waves split the work-group's block
+// tile holds (channels 32h + 8g .. +7 of column c, with the four channel groups of a column on
+// the four lanes of a quad: g = lane % 4, c = lane / 4; each load still covers one contiguous
+// KiB) with the same channels of every batch row, in fp32 with packed fp16/bf16 dot products,
+// and the quad is summed once at the end by two DPP quad permutes.  The waves split the work-group's block
 // list (as kind 1); each wave stages the activations of its own slice (BT rows x 64 channels per
 // block) in LDS once at the start, in [list position][row][half h][group g] 16-byte order, so
 // each of its later reads is a broadcast and the loop streams weights only.  A wave reads only
@@ -801,8 +849,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   int n0, n0y;
   if (!tile_columns<N2D>(p, tile, 16 * NSUB, &n0, &n0y)) return;
   const int y0 = blockIdx.y * BT;
+  BSG_TL_DECL
+  BSG_TL(0);
 
   const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * w) / WPG);
   const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
   const int cnt = pend - pbeg;
@@ -821,7 +872,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     qid[i] = s_ids[q < pend ? q : 0];
   }
   const int blk_bytes = p.npad * 128;
-  const int wcol = lane * 16 + (n0 >> 4) * 2048;
+  const int wcol = (lane & 3) * 256 + (lane >> 2) * 16 + (n0 >> 4) * 2048;  // quad layout
   u32x4 wv[DEPTH][NSUB][2];
   float acc[NSUB][BT];
 #pragma unroll
@@ -871,7 +922,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   // off the per-block path); XD shrinks as the batch tile grows to bound the registers.
   constexpr int XD = BT >= 8 ? 1 : (BT >= 4 ? 2 : DEPTH);
   static_assert(DEPTH % XD == 0, "X prefetch distance");
-  const int g = lane >> 4;
+  const int g = lane & 3;
   u32x4 xv[XD][2][BT];
   auto xread = [&](u32x4 (&xd)[2][BT], int t) {
     // Positions past the slice carry zero weights; read a valid X piece for them.
@@ -903,6 +954,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         compute(wv[d], xv[d % XD]);
+        BSG_TL_IF(2, t0 == 0 && d == 0);
         xread(xv[d % XD], t0 + d + XD);
         issue(wv[d], t0 + d + DEPTH);
         // Keep block d's loads between its dot products and block d+1's: left free, the
@@ -913,40 +965,172 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     }
   }
 
-  // Column c of subtile s: the lanes c, c+16, c+32, c+48 hold its four channel groups.
+  BSG_TL(3);
+  // Column c of subtile s: the quad of lanes 4c .. 4c+3 holds its four channel groups; two DPP
+  // quad permutes (swap neighbours, then swap pairs) leave the column's sum on every lane of the
+  // quad, (g0 + g1) + (g2 + g3) in a fixed order.
 #pragma unroll
   for (int s = 0; s < NSUB; ++s)
 #pragma unroll
     for (int b = 0; b < BT; ++b) {
       float v = acc[s][b];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xf, 0xf, false));
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xf, 0xf, false));
       acc[s][b] = v;
     }
+  const int qc = lane >> 2;  // the quad's column
   if constexpr (WPG > 1) {
-    if (w > 0 && lane < 16) {
+    if (w > 0 && (lane & 3) == 0) {
 #pragma unroll
       for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-        for (int b = 0; b < BT; ++b) s_red[w - 1][s * BT + b][lane] = acc[s][b];
+        for (int b = 0; b < BT; ++b) s_red[w - 1][s * BT + b][qc] = acc[s][b];
     }
     __syncthreads();
   }
-  if (w == 0 && lane < 16) {
+  if (w == 0 && (lane & 3) == 0) {
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      const int n = n0y + 16 * s + lane;
+      const int n = n0y + 16 * s + qc;
 #pragma unroll
       for (int b = 0; b < BT; ++b) {
         float v = acc[s][b];
-        for (int ww = 1; ww < WPG; ++ww) v += s_red[ww - 1][s * BT + b][lane];
+        for (int ww = 1; ww < WPG; ++ww) v += s_red[ww - 1][s * BT + b][qc];
         const int row = y0 + b;
         if (row < p.bt && n < p.ny) ((uint16_t*)p.y)[(size_t)row * (size_t)p.ldy + n] = Elem<T>::bits(v);
       }
     }
   }
+  BSG_TL(4);
+  BSG_TL_END(p, true);
 }
 
+
+// Column group t of G (kind 5): the N/16 subtiles are dealt out as evenly as possible, the
+// first T mod G groups taking one more, so any G (the compute-unit count) is filled whatever N is.
+__device__ __forceinline__ void vt_columns(int t, int G, int T, int* first, int* count) {
+  const int base = T / G;
+  const int extra = T - base * G;
+  *first = t * base + (t < extra ? t : extra);
+  *count = base + (t < extra ? 1 : 0);
+}
+
+// Kind 5 ("vt", variable-width tiles): one work-group = BTT*16 batch rows x nv <= NSUB 16-column
+// subtiles, nv from vt_columns.  Its 2*WB waves are (32-channel half h) x (block slice b): wave
+// (h, b) walks slice b of the list and, per block, loads the h-half of the weights of every
+// subtile (NSUB x 1 KiB) and the h-half activation fragment of every row tile (BTT x 1 KiB)
+// straight into registers.  Every weight and activation byte of the work-group is loaded by
+// exactly one wave; the loop has no LDS traffic and no barrier.  At the end the 2*WB partial
+// accumulators meet in LDS and wave w sums fragments w, w + 2*WB, ... in wave order and stores
+// them.  Activation bytes per weight byte: 16*BTT / (16*nv); 256 groups of 2-3 subtiles fill
+// 256 compute units at N = 11008 without split-K.
+// KH = 1 (kind 6): no channel-half split; each of the WB waves loads both halves of every
+// weight subtile and activation row tile of its blocks (the two halves of an activation row are
+// one 128-byte line, requested back to back by one wave).
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2>
+__global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p) {
+  constexpr int NW = KH * WB;
+  constexpr int NT = 64 * NW;
+  constexpr int F = BTT * NSUB;
+  constexpr int HP = 3 - KH;  // halves per wave
+  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
+  __shared__ __attribute__((aligned(16))) f32x4 s_red[NW][F][64];
+  __shared__ int s_misc[NW + 2];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = KH == 2 ? (w & 1) : 0;  // first channel half of this wave
+  const int b = KH == 2 ? (w >> 1) : w;  // block slice
+  int tile, sk;
+  tile_of_group(1, &tile, &sk);
+  int st, nv;
+  vt_columns(tile, p.n_tiles, p.npad >> 4, &st, &nv);
+  const int y0 = blockIdx.y * (16 * BTT);
+  BSG_TL_DECL
+  BSG_TL(0);
+
+  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  BSG_TL(1);
+  const int pbeg = (int)(((int64_t)na * b) / WB);
+  const int pend = (int)(((int64_t)na * (b + 1)) / WB);
+  const int cnt = pend - pbeg;
+
+  const int blk_bytes = p.npad * 128;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  int xrow_off[BTT];
+  bool xrow_ok[BTT];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi) {
+    const int row = y0 + 16 * bi + (lane & 15);
+    xrow_ok[bi] = row < p.bt;
+    xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
+  }
+  const int xcol = 32 * h + 8 * (lane >> 4);
+  int woff[NSUB];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) woff[s] = s < nv ? lane * 16 + (st + s) * 2048 + h * 1024 : kOOB;
+
+  u32x4 wv[DEPTH][NSUB][HP];
+  u32x4 xv[DEPTH][BTT][HP];
+  f32x4 acc[BTT][NSUB];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](u32x4 (&wd)[NSUB][HP], u32x4 (&xd)[BTT][HP], int t) {
+    const int q = t < cnt ? pbeg + t : 0;
+    int blk = s_ids[q];
+    blk = __builtin_amdgcn_readfirstlane(blk);
+    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
+    const int col = (ok ? blk : 0) * 64 + xcol;
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh) {
+        const bool v = ok && xrow_ok[bi] && col + 32 * hh < p.K;
+        xd[bi][hh] = ld16(xr, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+      }
+  };
+
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
+  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh)
+#pragma unroll
+        for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xv[d][bi][hh], acc[bi][s]);
+      BSG_TL_IF(2, t0 == 0 && d == 0);
+      issue(wv[d], xv[d], t0 + d + DEPTH);
+    }
+  }
+  BSG_TL(3);
+
+  // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read: s_red is separate).
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) s_red[w][bi * NSUB + s][lane] = acc[bi][s];
+  __syncthreads();
+  for (int f = w; f < F; f += NW) {
+    f32x4 v = s_red[0][f][lane];
+#pragma unroll
+    for (int ww = 1; ww < NW; ++ww) v += s_red[ww][f][lane];
+    if (f % NSUB < nv) store_y<T, NSUB>(p, y0, st * 16, f, v);
+  }
+  BSG_TL(4);
+  BSG_TL_END(p, true);
+}
 
 // The 2-D instantiation of a tile, or null when its work-group covers more than one 64-column
 // output block (the discarded branch is never instantiated).
@@ -977,6 +1161,12 @@ constexpr GemmFn kernel_2d() {
   {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false>,        \
    bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D, false>, kernel_2d<KIND_XLDS_KH, _Float16, B, S, W, D>(), \
    kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>()}
+#define BSG_V(B, S, W, D)                                                                               \
+  {KIND_VT, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W / 2, D>, bsg_gemm_vt_kernel<__bf16, B, S, W / 2, D>, \
+   nullptr, nullptr}
+#define BSG_V1(B, S, W, D)                                                                                \
+  {KIND_VT1, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1>, bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1>, \
+   nullptr, nullptr}
 #define BSG_F(R, S, W, D)                                                                                 \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
    kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>()}

@@ -431,7 +431,8 @@ __global__ __launch_bounds__(1024) void bsg_nmask_kernel(const uint8_t* __restri
 }
 
 // The whole instantiated tile set, one table per translation unit.
-const TileTable* const kTables[] = {&kTilesK1R16, &kTilesK1R32, &kTilesK1R64, &kTilesK2, &kTilesK4, &kTilesK3};
+const TileTable* const kTables[] = {&kTilesK1R16, &kTilesK1R32, &kTilesK1R64, &kTilesK2, &kTilesK4, &kTilesK3,
+                                    &kTilesK5};
 
 const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
   for (const TileTable* t : kTables)
@@ -459,7 +460,8 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
 
-// Columns covered by one work-group of a resolved plan.
+// Columns covered by one work-group of a resolved plan (kind 5: at most; its groups take the
+// floor or ceiling of an even share).
 int64_t group_cols(const bsg_plan* pl) {
   if (pl->kind == KIND_XLDS) return (int64_t)pl->cols_per_wave * pl->waves_per_group;
   if (pl->kind == KIND_XLDS_KH) return (int64_t)pl->cols_per_wave * (pl->waves_per_group / 2);
@@ -488,13 +490,47 @@ int resolve_fma(int64_t bt, int32_t na, bsg_plan* pl) {
   return BSG_OK;
 }
 
+// Kind 5 and 6 plans: explicit or tuned only; no split-K (their groups already fill the chip).
+int resolve_vt(bsg_plan* pl) {
+  const int rpg = pl->rows_per_group;
+  if (rpg != 16 && rpg != 32 && rpg != 64)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind %d rows_per_group=%d (16, 32 or 64)", pl->kind, rpg);
+  if (pl->split_k == 0) pl->split_k = 1;
+  if (pl->split_k != 1)
+    return fail(BSG_ERR_UNSUPPORTED, "plan: kind %d needs split_k=1 (got %d)", pl->kind, pl->split_k);
+  if (pl->cols_per_wave == 0) pl->cols_per_wave = 48;
+  if (pl->waves_per_group == 0) pl->waves_per_group = 4;
+  if (pl->depth == 0) pl->depth = 4;
+  if (pl->cols_per_wave % 16 != 0 ||
+      !find_kernel(pl->kind, rpg, pl->cols_per_wave / 16, pl->waves_per_group, pl->depth))
+    return fail(BSG_ERR_UNSUPPORTED, "plan: no kind %d kernel for rows_per_group=%d cols_per_wave=%d "
+                "waves_per_group=%d depth=%d", pl->kind, rpg, pl->cols_per_wave, pl->waves_per_group, pl->depth);
+  return BSG_OK;
+}
+
+// Kind 5 column groups: every compute unit (per row group) gets one, unless that would leave a
+// group more than the plan's subtiles; never more groups than subtiles.
+int64_t vt_groups(int64_t N, int64_t ygroups, int32_t cu, const bsg_plan* pl) {
+  const int64_t T = cdiv(N, 16);
+  const int64_t nsub = pl->cols_per_wave / 16;
+  int64_t g = cu / ygroups;
+  if (g < cdiv(T, nsub)) g = cdiv(T, nsub);
+  if (g > T) g = T;
+  return g < 1 ? 1 : g;
+}
+
 int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_plan* pl) {
   if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
     return fail(BSG_ERR_ARG, "plan: bt=%lld N=%lld nblk=%d na=%d cu=%d", (long long)bt, (long long)N,
                 nblk, na, cu);
-  if (pl->kind < 0 || pl->kind > KIND_XLDS_KH)
+  if (pl->kind < 0 || pl->kind > KIND_VT1)
     return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X tile in LDS, "
-                "3 = fp32 dot products for 1-8 rows, 4 = as 2 with channel-half waves)", pl->kind);
+                "3 = fp32 dot products for 1-8 rows, 4 = as 2 with channel-half waves, 5 = variable-width "
+                "column groups, 6 = as 5 with waves splitting blocks only)", pl->kind);
+  if (pl->kind == KIND_VT || pl->kind == KIND_VT1) {
+    if (pl->rows_per_group == 0) pl->rows_per_group = bt <= 16 ? 16 : (bt <= 32 ? 32 : 64);
+    return resolve_vt(pl);
+  }
   // The dot-product kernel (kind 3) runs when a plan names it; automatic plans use the MFMA
   // kinds, which measure faster at every batch size on gfx950.
   if (pl->rows_per_group == 0 && pl->kind == KIND_FMA) pl->rows_per_group = bt <= 8 ? pow2_ceil(bt) : 8;
@@ -627,6 +663,23 @@ int check_common(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* 
   return BSG_OK;
 }
 
+#ifdef BSG_TIMELINE
+// Profiling build: launches write their work-groups' phase stamps to consecutive slots of a
+// caller buffer (bsg_timeline_attach), slot = launch count modulo the slot count, so the R
+// launches of a captured graph each keep their own slot across replays.
+uint64_t* g_tl_base = nullptr;
+int64_t g_tl_slots = 0, g_tl_slot_groups = 0, g_tl_next = 0;
+
+uint64_t* timeline_slot(int64_t groups) {
+  if (g_tl_base == nullptr || groups > g_tl_slot_groups) return nullptr;
+  uint64_t* t = g_tl_base + (g_tl_next % g_tl_slots) * g_tl_slot_groups * 8;
+  ++g_tl_next;
+  return t;
+}
+#else
+uint64_t* timeline_slot(int64_t) { return nullptr; }
+#endif
+
 // Optional parts of a launch.  MODE_TOPK: the exact-L1 block scores (na is then k), and where
 // work-group (0, 0) publishes the kept list and its count (null: not published).  2-D
 // sparsity: the active 64-column output blocks nidx[nn] (device; nn_dev, when set, a device
@@ -706,8 +759,12 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
     return fail(BSG_ERR_UNSUPPORTED, "2-D: the plan covers %lld columns per work-group (at most 64: "
                 "cols_per_wave x column waves)", (long long)gc);
   // 2-D: 64 / gc tiles per active output block (a device-side count leaves tiles idle)
-  const int64_t n_tiles = ex.nidx != nullptr ? (int64_t)ex.nn * (64 / gc) : cdiv(npad, gc);
   const int64_t ygroups = cdiv(bt, pl.rows_per_group);
+  const bool vt = pl.kind == KIND_VT || pl.kind == KIND_VT1;
+  if (vt && ex.nidx != nullptr)
+    return fail(BSG_ERR_UNSUPPORTED, "2-D: kinds 5 and 6 (variable-width column groups) have no 2-D form");
+  const int64_t n_tiles = vt ? vt_groups(N, ygroups, device_cu_count(), &pl)
+                          : ex.nidx != nullptr ? (int64_t)ex.nn * (64 / gc) : cdiv(npad, gc);
   if (n_tiles * pl.split_k > 0x7fffffff || ygroups > 65535) return fail(BSG_ERR_UNSUPPORTED, "grid too large");
 
   GemmParams p;
@@ -717,7 +774,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.idx = idx;
   p.na_dev = na_dev;
   p.bitmap = bitmap;
-  if (n_tiles * ygroups > ws_max_tiles(bt, N, &pl))
+  if (need > 0 && n_tiles * ygroups > ws_max_tiles(bt, N, &pl))
     return fail(BSG_ERR_UNSUPPORTED, "%lld output tiles exceed the workspace layout", (long long)(n_tiles * ygroups));
   p.cnt = need > 0 ? (fixed_ws ? ex.cnt_fixed : (uint32_t*)ws) : nullptr;
   p.part = need > 0 ? (fixed_ws ? ex.part_fixed : (float*)((char*)ws + ws_counter_bytes(bt, N, &pl))) : nullptr;
@@ -744,6 +801,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.nn_dev = ex.nn_dev;
   p.nn = ex.nn;
   p.ncompact = ex.ncompact;
+  p.tl = timeline_slot((int64_t)n_tiles * pl.split_k * ygroups);
 
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
@@ -1143,6 +1201,33 @@ int bsg_select_gemm_noalloc(const void* x, int64_t ldx, int64_t bt, int64_t K, i
   fx.part_cap_bytes = BSG_NOALLOC_SCRATCH_BYTES - kScratchPartOff;
   return select_gemm_run(x, ldx, bt, K, k, wp, N, idx_out, na_out, y, ldy, dtype,
                          (uint64_t*)(base + kScratchCntBytes), nullptr, 0, fx, plan, stream);
+}
+
+#ifdef BSG_TIMELINE
+// Profiling build only (include/bsgemm_timeline.h): later GEMM launches record phase stamps into
+// buf, `slots` launches of up to `slot_groups` work-groups each (8 uint64 per work-group), cycling.
+// buf = NULL detaches.  Returns BSG_OK or BSG_ERR_ARG.
+int bsg_timeline_attach(void* buf, int64_t slots, int64_t slot_groups) {
+  if (buf != nullptr && (slots <= 0 || slot_groups <= 0 || ((uintptr_t)buf & 7u) != 0))
+    return fail(BSG_ERR_ARG, "timeline: slots=%lld slot_groups=%lld", (long long)slots, (long long)slot_groups);
+  g_tl_base = (uint64_t*)buf;
+  g_tl_slots = buf ? slots : 0;
+  g_tl_slot_groups = buf ? slot_groups : 0;
+  g_tl_next = 0;
+  return BSG_OK;
+}
+#else
+int bsg_timeline_attach(void* buf, int64_t, int64_t) {
+  if (buf == nullptr) return BSG_OK;
+  return fail(BSG_ERR_UNSUPPORTED, "timeline: this is not the profiling build (libbsgemm_timeline.so)");
+}
+#endif
+
+int64_t bsg_timeline_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return -1;
+  return khz;
 }
 
 }  // extern "C"
