@@ -70,6 +70,9 @@ def parse_args():
     ap.add_argument("--workload", default="llama",
                     choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d", "timeline"])
     ap.add_argument("--plan", default=None, help="timeline workload: explicit plan a,b,c,d,e,f (default: tuned)")
+    ap.add_argument("--select", action="store_true",
+                    help="timeline workload: the exact-L1 selection + GEMM (k = the point's blocks); stamps "
+                         "cover the GEMM launch")
     ap.add_argument("--batches", default=None, help="perstep workload: batch sizes (default: all six)")
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
@@ -922,6 +925,17 @@ def run_timeline(args, dev):
     rf, ok = pt.check()
     if not ok:
         raise SystemExit(f"{name}: parity failure (rel_fro {rf})")
+    if args.select:
+        from bsa_mi355x.select import select_gemm_packed
+
+        sel_idx = torch.empty(na, dtype=torch.int32, device=dev)
+        sel_cnt = torch.empty(1, dtype=torch.int32, device=dev)
+
+        def launch_select(i):
+            select_gemm_packed(pt.x, pool.packed[i % pt.copies], pt.n, na, pt.y, plan=pt.plan, idx_out=sel_idx,
+                               count_out=sel_cnt, workspace_prefix="tl_select")
+
+        pt.launch = launch_select
     groups = 1 << 16
     buf = torch.zeros(pt.copies * groups * 8, dtype=torch.int64, device=dev)
     rc = lib.bsg_timeline_attach(buf.data_ptr(), pt.copies, groups)

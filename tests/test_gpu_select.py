@@ -99,6 +99,9 @@ def _fused(dev, x, w_nk, k, plan=None):
     (8, 32768, 256, 100, (1, 16, 1, 4, 16, 1)),   # 512 blocks: rank launch
     (4, 38400, 256, 77, None),                    # 600 blocks: rank launch
     (16, 4096, 512, 0, None), (16, 4096, 512, 64, None), (16, 4096, 512, 200, None),
+    (64, 4096, 11008, 31, (1, 48, 2, 4, 64, 6)),  # variable-width groups, waves split blocks
+    (16, 4096, 12288, 23, (1, 48, 4, 4, 16, 5)),  # variable-width groups, channel-half waves
+    (64, 4096, 22016, 31, (1, 96, 2, 4, 64, 5)),  # 5-6 subtiles per group
 ])
 def test_fused_select_gemm_every_kind(dev, bt, kdim, n, k, plan):
     """Selection + GEMM for every kernel kind and edge k, with the top-k either ranked inside
@@ -246,3 +249,4 @@ def test_reference_drop_ins_ignore_a_prior_of_the_wrong_length(dev):
     got = bsa._select_active_blocks(x3, 0.3, 64, block_prior=prior).cpu().numpy()
     want, _, _ = orc.select_scored_ref(x, orc.n_keep(0.3, 64), "l2_mean", prior=prior.cpu().numpy())
     assert np.array_equal(got, want) and not np.array_equal(got, base)
+
