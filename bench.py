@@ -51,7 +51,11 @@ X_DIST = {"qkvo": "normal", "gate_up": "normal", "down": "laplace"}
 # Committed PMC summaries (HBM bytes per launch) of the roofline point of each workload.
 TRAFFIC_PROFILES = {
     "down_b16_s500": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md"),
-    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_xl_gate_up_b64_s520.md"),
+    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_vt_gate_up_b64_s520.md"),
+}
+# MFMA utilisation from counters (SQ_VALU_MFMA_BUSY_CYCLES) of the roofline point's kernel.
+MFMA_PROFILES = {
+    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_gate_up_b64_s520.md"),
 }
 # Kernel (symbol prefix) that each plan kind launches.
 KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel",
@@ -69,7 +73,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="llama",
                     choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d", "timeline"])
-    ap.add_argument("--plan", default=None, help="timeline workload: explicit plan a,b,c,d,e,f (default: tuned)")
+    ap.add_argument("--plan", default=None,
+                    help="timeline workload, or llama/down_sweep with --only: explicit plan a,b,c,d,e,f "
+                         "(default: tuned)")
     ap.add_argument("--select", action="store_true",
                     help="timeline workload: the exact-L1 selection + GEMM (k = the point's blocks); stamps "
                          "cover the GEMM launch")
@@ -307,20 +313,31 @@ def cpu_point_us(point, runs=5):
     return statistics.median(samples)
 
 
-def load_traffic(point):
-    """HBM bytes per launch of a roofline point, from its committed PMC summary (a line
-    `traffic_bytes_per_launch: <int>`), or None when that point has no summary."""
-    path = TRAFFIC_PROFILES.get(point)
+def _profile_value(path, key, conv):
+    """The `key: value` line of a committed profile summary, or None."""
     if path is None:
         return None
     try:
         with open(path) as f:
             for line in f:
-                if line.strip().startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                if line.strip().startswith(key + ":"):
+                    return conv(line.split(":", 1)[1].strip())
     except (OSError, ValueError):
         pass
     return None
+
+
+def load_mfma_util(point):
+    """Counter-measured MFMA utilisation of a roofline point's kernel (committed PMC summary)."""
+    path = MFMA_PROFILES.get(point)
+    v = _profile_value(path, "mfma_util_counter", float)
+    return None if v is None else {"value": v, "profile": os.path.relpath(path, ROOT)}
+
+
+def load_traffic(point):
+    """HBM bytes per launch of a roofline point, from its committed PMC summary (a line
+    `traffic_bytes_per_launch: <int>`), or None when that point has no summary."""
+    return _profile_value(TRAFFIC_PROFILES.get(point), "traffic_bytes_per_launch", int)
 
 
 def copy_calibration(mib, steps):
@@ -452,10 +469,17 @@ def run_matrix(args, dev):
         nas = sorted({na for _, s2, b2, na, _ in rows if (s2, b2) == key})
         x, _, masks = orc.make_inputs(SEED, key[1], *SHAPES[key[0]], X_DIST[key[0]], na=nas)
         drawn[key] = (x, dict(zip(nas, masks)))
+    forced = None
+    if args.plan:
+        if not args.only:
+            raise SystemExit("--plan needs --only")
+        import bsa_mi355x as bsa
+
+        forced = bsa.Plan(*[int(v) for v in args.plan.split(",")])
     points = []
     for name, sh, bt, na, dense in rows:
         x, masks = drawn[(sh, bt)]
-        points.append(Point(name, pools[sh], bt, na, dev, dense=dense, inputs=(x, masks[na])))
+        points.append(Point(name, pools[sh], bt, na, dev, dense=dense, plan=forced, inputs=(x, masks[na])))
         log(f"prepared {name}: na={points[-1].na} copies={points[-1].copies} "
             f"replay={points[-1].replay_bytes / 2**30:.2f} GiB plan={points[-1].plan}")
     bad = []
@@ -509,6 +533,9 @@ def run_matrix(args, dev):
                 "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
                 "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes,
                 "plan": list(fp.plan.as_tuple())}
+    mf = load_mfma_util(focus)
+    if mf is not None:
+        roofline["mfma_util_counter"] = mf
     if not args.only:
         rd = read_calibration_us(fp)
         roofline["practical_read"] = {

@@ -172,6 +172,25 @@ def test_bench_traffic_profile_per_roofline_point():
     assert bench.load_traffic("qkvo_b2_s803") is None
 
 
+def test_bench_roofline_profiles_match_the_tuned_kernel():
+    """The committed traffic and counter summaries of the llama roofline point were taken on the
+    kernel its tuned plan launches now (a retune that changes the kernel makes them stale)."""
+    bench = _bench_module()
+    from bsa_mi355x import tuning
+
+    plan = tuning.lookup(64, 11008, 64, 31)
+    assert plan is not None
+    kern = bench.KERNEL_NAMES[plan.kind]
+    for prof in (bench.TRAFFIC_PROFILES["gate_up_b64_s520"], bench.MFMA_PROFILES["gate_up_b64_s520"]):
+        with open(prof) as f:
+            text = f.read()
+        assert kern in text, (prof, kern)
+        assert ",".join(str(v) for v in plan.as_tuple()) in text.replace(" ", ""), (prof, plan)
+    mf = bench.load_mfma_util("gate_up_b64_s520")
+    assert mf is not None and 0.0 < mf["value"] < 1.0
+    assert bench.load_mfma_util("qkvo_b2_s803") is None
+
+
 def _bench_module():
     import importlib.util
 
