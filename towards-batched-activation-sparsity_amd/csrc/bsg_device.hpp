@@ -587,10 +587,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto issue = [&](u32x4 (&wd)[NSUB][2], u32x4 (&xd)[BTT][2], int t) {
-    const int q = t < cnt ? pbeg + t : 0;
+    const bool in = (unsigned)t < (unsigned)cnt;
+    const int q = in ? pbeg + t : 0;
     int blk = s_ids[q];
     blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
@@ -619,16 +620,28 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
         for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][h], xd[bi][h], acc[bi][s]);
   };
 
-  // Rolling pipeline: DEPTH blocks in flight; loads past the slice are out-of-range (zero,
-  // no memory traffic) so the body has no data-dependent branches.
+  // Rolling pipeline, DEPTH blocks in flight, over U = cnt rounded up to DEPTH slots: slot u
+  // holds list entry u - pad, so the pad leading slots are out-of-range loads (zero, no memory
+  // traffic) issued with the first real ones, the passes have no data-dependent branches, and
+  // the last pass only drains (no load is in flight when the loop ends).
+  if (cnt > 0) {
+    const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
+    const int U = cnt + pad;
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
-  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+    for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d - pad);
+    int u0 = 0;
+    for (; u0 + DEPTH < U; u0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute(wv[d], xv[d]);
+        BSG_TL_IF(2, u0 + d == pad);
+        issue(wv[d], xv[d], u0 + d + DEPTH - pad);
+      }
+    }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       compute(wv[d], xv[d]);
-      BSG_TL_IF(2, t0 == 0 && d == 0);
-      issue(wv[d], xv[d], t0 + d + DEPTH);
+      BSG_TL_IF(2, u0 + d == pad);
     }
   }
   BSG_TL(3);
@@ -741,10 +754,11 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto issue = [&](u32x4 (&wd)[NSUB][HPW], u32x4 (&xd)[XPW], int t) {
-    const int q = t < cnt ? pbeg + t : 0;
+    const bool in = (unsigned)t < (unsigned)cnt;
+    const int q = in ? pbeg + t : 0;
     int blk = s_ids[q];
     blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
@@ -760,30 +774,46 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
     }
   };
 
+  // Slot u: publish its X (LDS stage u & 1); after the barrier every wave has also finished
+  // reading the stage it will overwrite at slot u + 1.
+  auto consume = [&](const u32x4 (&wd)[NSUB][HPW], const u32x4 (&xd)[XPW], int u) {
+    const int stage = u & 1;
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xs[d], d);
-  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+    for (int j = 0; j < XPW; ++j)
+      if (w + j * WPG < XF) s_x[stage][w + j * WPG][lane] = xd[j];
+    __syncthreads();
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = WK > 1 ? wk : hh;
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi) {
+        const u32x4 xb = s_x[stage][2 * bi + h][lane];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][hh], xb, acc[bi][s]);
+      }
+    }
+  };
+
+  // Rolling pipeline as in kind 1 (leading out-of-range slots, branch-free passes, a drain).
+  // Every wave walks the same slice, so all take the same passes and barriers.
+  if (cnt > 0) {
+    const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
+    const int U = cnt + pad;
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(wv[d], xs[d], d - pad);
+    int u0 = 0;
+    for (; u0 + DEPTH < U; u0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        consume(wv[d], xs[d], u0 + d);
+        BSG_TL_IF(2, u0 + d == pad);
+        issue(wv[d], xs[d], u0 + d + DEPTH - pad);
+      }
+    }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int stage = (t0 + d) & 1;
-      // Publish X of block t0+d; after the barrier every wave has also finished reading the
-      // stage it will overwrite next iteration.
-#pragma unroll
-      for (int j = 0; j < XPW; ++j)
-        if (w + j * WPG < XF) s_x[stage][w + j * WPG][lane] = xs[d][j];
-      __syncthreads();
-#pragma unroll
-      for (int hh = 0; hh < HPW; ++hh) {
-        const int h = WK > 1 ? wk : hh;
-#pragma unroll
-        for (int bi = 0; bi < BTT; ++bi) {
-          const u32x4 xb = s_x[stage][2 * bi + h][lane];
-#pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xb, acc[bi][s]);
-        }
-      }
-      BSG_TL_IF(2, t0 == 0 && d == 0);
-      issue(wv[d], xs[d], t0 + d + DEPTH);
+      consume(wv[d], xs[d], u0 + d);
+      BSG_TL_IF(2, u0 + d == pad);
     }
   }
   BSG_TL(3);
@@ -881,10 +911,11 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     for (int b = 0; b < BT; ++b) acc[s][b] = 0.f;
 
   auto issue = [&](u32x4 (&wd)[NSUB][2], int t) {
-    const int qq = t < cnt ? pbeg + t : 0;
+    const bool in = (unsigned)t < (unsigned)cnt;
+    const int qq = in ? pbeg + t : 0;
     int blk = s_ids[qq];
     blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
@@ -908,8 +939,12 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
       xs[i] = ld16(xr, v ? row * (int)p.ldx * 2 + col * 2 : kOOB);
     }
   }
+  // Rolling pipeline as in kind 1: slot u holds list entry u - pad (leading out-of-range
+  // slots), branch-free passes, a drain.
+  const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
+  const int U = cnt + pad;
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d);
+  for (int d = 0; d < DEPTH; ++d) issue(wv[d], d - pad);
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int e = i * 64 + lane;
@@ -925,8 +960,8 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   const int g = lane & 3;
   u32x4 xv[XD][2][BT];
   auto xread = [&](u32x4 (&xd)[2][BT], int t) {
-    // Positions past the slice carry zero weights; read a valid X piece for them.
-    const int q = pbeg + (t < cnt ? t : cnt - 1);
+    // Positions outside the slice carry zero weights; read a valid X piece for them.
+    const int q = pbeg + (t < 0 ? 0 : (t < cnt ? t : cnt - 1));
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -949,19 +984,26 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
 
   if (cnt > 0) {
 #pragma unroll
-    for (int k = 0; k < XD; ++k) xread(xv[k], k);
-    for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+    for (int k = 0; k < XD; ++k) xread(xv[k], k - pad);
+    int u0 = 0;
+    for (; u0 + DEPTH < U; u0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         compute(wv[d], xv[d % XD]);
-        BSG_TL_IF(2, t0 == 0 && d == 0);
-        xread(xv[d % XD], t0 + d + XD);
-        issue(wv[d], t0 + d + DEPTH);
+        BSG_TL_IF(2, u0 + d == pad);
+        xread(xv[d % XD], u0 + d + XD - pad);
+        issue(wv[d], u0 + d + DEPTH - pad);
         // Keep block d's loads between its dot products and block d+1's: left free, the
         // scheduler gathers every dot product of the pass above every load, so each pass
         // starts by waiting for all DEPTH blocks in flight and the pipeline drains.
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(wv[d], xv[d % XD]);
+      BSG_TL_IF(2, u0 + d == pad);
+      if (d + XD < DEPTH) xread(xv[d % XD], u0 + d + XD - pad);
     }
   }
 
@@ -1079,10 +1121,11 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto issue = [&](u32x4 (&wd)[NSUB][HP], u32x4 (&xd)[BTT][HP], int t) {
-    const int q = t < cnt ? pbeg + t : 0;
+    const bool in = (unsigned)t < (unsigned)cnt;
+    const int q = in ? pbeg + t : 0;
     int blk = s_ids[q];
     blk = __builtin_amdgcn_readfirstlane(blk);
-    const bool ok = (t < cnt) && blk >= 0 && blk < p.nblk;
+    const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
 #pragma unroll
@@ -1099,19 +1142,34 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
       }
   };
 
+  auto compute = [&](const u32x4 (&wd)[NSUB][HP], const u32x4 (&xd)[BTT][HP]) {
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d);
-  for (int t0 = 0; t0 < cnt; t0 += DEPTH) {
+    for (int hh = 0; hh < HP; ++hh)
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][hh], xd[bi][hh], acc[bi][s]);
+  };
+
+  // Rolling pipeline as in kind 1: leading out-of-range slots, branch-free passes, a drain.
+  if (cnt > 0) {
+    const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
+    const int U = cnt + pad;
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d - pad);
+    int u0 = 0;
+    for (; u0 + DEPTH < U; u0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute(wv[d], xv[d]);
+        BSG_TL_IF(2, u0 + d == pad);
+        issue(wv[d], xv[d], u0 + d + DEPTH - pad);
+      }
+    }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh)
-#pragma unroll
-        for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xv[d][bi][hh], acc[bi][s]);
-      BSG_TL_IF(2, t0 == 0 && d == 0);
-      issue(wv[d], xv[d], t0 + d + DEPTH);
+      compute(wv[d], xv[d]);
+      BSG_TL_IF(2, u0 + d == pad);
     }
   }
   BSG_TL(3);
