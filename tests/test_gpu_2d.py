@@ -165,6 +165,22 @@ def test_2d_rejects_a_wide_plan(dev):
     x, w_nk, kb = case(65, bt, kdim, n, 10, "normal")
     with pytest.raises(ValueError):
         _run(dev, x, w_nk, kb, [1], False, plan=(1, 32, 4, 4, 32, 2))  # 128 columns per work-group
+    with pytest.raises(ValueError):
+        _run(dev, x, w_nk, kb, [1], False, plan=(1, 48, 2, 4, 32, 6))  # variable-width groups: no 2-D kernel
+
+
+@pytest.mark.parametrize("bt,na", [(4, 6), (4, 25), (16, 23), (64, 31)])
+def test_2d_auto_plan_when_the_tuned_1d_plan_is_variable_width(dev, bt, na):
+    """The automatic 2-D plan starts from the tuned 1-D plan of the same problem; where that is a
+    variable-width kind (5/6, no 2-D instantiation) it takes the 16-column list-splitting tile
+    of the same rows instead, with its own split-K, and matches the oracle."""
+    from bsa_mi355x import sparse2d as s2d_mod
+
+    kdim, n = 4096, 4096
+    x, w_nk, kb = case(90 + bt, bt, kdim, n, na, "normal")
+    pl = s2d_mod.plan_2d(bt, n, 3, orc.nblk_of(kdim), na, dev)
+    assert pl.kind in (1, 2, 3, 4) and pl.group_cols() <= 64, pl
+    _check(_run(dev, x, w_nk, kb, [0, 17, 63], False), x, w_nk, kb, [0, 17, 63], False, f"auto 2-D B={bt} na={na}")
 
 
 def test_every_2d_tile(dev):

@@ -364,6 +364,40 @@ def test_strided_rows_and_side_stream(dev, plan):
     assert_close(y[:, :n], orc.gemm_ref64(x, w_nk, idx), f"strided {plan}")
 
 
+@pytest.mark.parametrize("bt,plan", [
+    (5, (1, 16, 4, 4, 16, 1)),    # kind 1: 4 waves, each its own slice
+    (5, (3, 16, 2, 8, 16, 1)),    # kind 1 under split-K 3, depth 8
+    (20, (2, 16, 4, 8, 32, 2)),   # kind 2: waves share the slice (per-block barrier)
+    (40, (1, 16, 8, 4, 64, 4)),   # kind 4
+    (3, (1, 16, 4, 4, 4, 3)),     # kind 3
+    (9, (1, 48, 4, 4, 16, 5)),    # kind 5
+    (50, (1, 48, 2, 4, 64, 6)),   # kind 6
+])
+def test_pipeline_every_slice_length(dev, bt, plan):
+    """Each wave's slice is rounded up to the prefetch depth with leading out-of-range slots and
+    the last pass only drains: every active count from 0 to past 2 x waves x depth, so every
+    slice length mod depth (and slices shorter than the depth) occurs in every kernel kind."""
+    k, n = 64 * 48, 112
+    nblk = orc.nblk_of(k)
+    x, w_nk, _ = case(31 + bt, bt, k, n, 1, "normal")
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    p = bsa.Plan(*plan)
+    splitters = p.split_k * (p.waves_per_group if p.kind in (1, 3) else 1) * \
+        (p.waves_per_group // 2 if p.kind == 5 else (p.waves_per_group if p.kind == 6 else 1))
+    top = min(nblk, 2 * splitters * p.depth + p.depth + 1)
+    rng = np.random.default_rng(bt)
+    for na in range(0, top + 1):
+        idx = np.sort(rng.choice(nblk, size=na, replace=False)).astype(np.int32)
+        out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        print(f"pipeline plan={plan} bt={bt} na={na}", flush=True)
+        used = bsa.gemm_packed(xt, packed, n, to_dev(idx, dev) if na else torch.empty(0, dtype=torch.int32, device=dev),
+                               out, plan=p, workspace_prefix="pipe")
+        assert used.as_tuple() == p.as_tuple(), used
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx), f"plan {plan} na={na}")
+
+
 @pytest.mark.parametrize("bt,k,n,na", [(64, 4096, 11008, 31), (37, 4096, 11008, 23), (16, 4096, 11008, 23),
                                        (2, 4096, 11008, 13), (64, 11008, 4096, 83), (33, 4096, 12288, 31),
                                        (16, 4096, 22016, 31), (5, 1000, 1000, 7)])

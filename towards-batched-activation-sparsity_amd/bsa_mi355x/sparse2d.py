@@ -56,6 +56,13 @@ def plan_2d(bt: int, n_dim: int, nn: int, nblk: int, na: int, device: torch.devi
     down_proj B=16 and B=64 with 16-64 of 64 output blocks."""
     explicit = plan is not None and any(plan.as_tuple())
     pl = resolve_plan(bt, n_dim, nblk, na, device, plan, dense=dense)
+    if pl.kind in (5, 6):
+        # variable-width column groups have no 2-D instantiation: the 16-column list-splitting
+        # tile of the same rows instead
+        if explicit:
+            raise ValueError(f"2-D sparsity runs kinds 1-4; plan {pl.as_tuple()} is kind {pl.kind}")
+        pl = resolve_plan(bt, n_dim, nblk, na, device, Plan(1, 16, 0, 0, pl.rows_per_group, 1), dense=dense,
+                          lookup_plan=False)
     if pl.group_cols() > BLOCK_N_OUT:
         if explicit:
             raise ValueError(f"2-D sparsity needs a plan covering at most {BLOCK_N_OUT} columns per work-group; "
