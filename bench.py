@@ -930,7 +930,9 @@ def run_timeline(args, dev):
     0 stamping the 100 MHz wall clock at its phase boundaries).  The point's R rotated launches are
     captured as one graph (the bench's rotation) and replayed; the stamps of the last replay give,
     per launch, each work-group's phases relative to the launch's first work-group start:
-    dispatch skew, list staging, first block consumed, main loop, epilogue, hand-off/end.  Also
+    dispatch skew, list staging, first block consumed, main loop (wave 0), how long after wave 0
+    the work-group's last wave ended its loop (last_wave_lag, inside the epilogue), epilogue,
+    hand-off/end.  Also
     reports the per-launch time of the graph, whose excess over the stamped span is the gap
     between kernels."""
     import numpy as np
@@ -987,8 +989,8 @@ def run_timeline(args, dev):
     per_launch = statistics.median(ts)
     st = buf.view(pt.copies, groups, 8).cpu().numpy()
     us = 1e3 / khz
-    phases = {"dispatch_skew": [], "list_staging": [], "first_block": [], "main_loop": [], "epilogue": [],
-              "handoff_end": [], "end_offset": []}
+    phases = {"dispatch_skew": [], "list_staging": [], "first_block": [], "main_loop": [], "last_wave_lag": [],
+              "epilogue": [], "handoff_end": [], "end_offset": []}
     last = {"handoff_end": [], "end_offset": []}
     spans, end_spread = [], []
     n_groups = 0
@@ -1007,10 +1009,12 @@ def run_timeline(args, dev):
         first = np.where(g[:, 2] > 0, g[:, 2], g[:, 3])
         phases["first_block"] += list((first - g[:, 1]) * us)
         phases["main_loop"] += list((g[:, 3] - first) * us)
+        last_end = g[:, 6] >> 1  # the work-group's last wave to end its main loop
+        phases["last_wave_lag"] += list((np.maximum(last_end, g[:, 3]) - g[:, 3]) * us)
         phases["epilogue"] += list((g[:, 4] - g[:, 3]) * us)
         phases["handoff_end"] += list((g[:, 5] - g[:, 4]) * us)
         phases["end_offset"] += list((g[:, 5] - t0) * us)
-        ly = g[:, 6] == 1
+        ly = (g[:, 6] & 1) == 1
         last["handoff_end"] += list((g[ly, 5] - g[ly, 4]) * us)
         last["end_offset"] += list((g[ly, 5] - t0) * us)
     summary = {k: {"median": round(float(np.median(v)), 3), "p10": round(float(_pct(v, 0.1)), 3),

@@ -8,7 +8,8 @@
  * per work-group g, 8 uint64 at buf[(launch % slots) * slot_groups * 8 + g * 8 + i]:
  *   i = 0 entry, 1 block list staged, 2 first block's weights consumed, 3 main loop done,
  *       4 outputs or partials issued, 5 end (own stores acknowledged)   -- 100 MHz wall clock
- *   i = 6 1 when the work-group stored Y (under split-K: the last arriver of its tile), else 0
+ *   i = 6 bit 0: 1 when the work-group stored Y (under split-K: the last arriver of its tile);
+ *         bits 1..63: the latest main-loop end (same clock) over the work-group's waves
  *   i = 7 (XCC id << 32) | HW_ID register
  * Launches with more than slot_groups work-groups record nothing.  buf = NULL detaches.
  * The shipped libbsgemm.so exports the same symbol and returns BSG_ERR_UNSUPPORTED for any

@@ -81,20 +81,31 @@ constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, 
 // clock at its phase boundaries in registers and writes them once at the end to
 // p.tl[group * 8 + slot]: 0 entry, 1 block list staged, 2 first block's weights consumed,
 // 3 main loop done, 4 outputs or partials issued, 5 end (own stores acknowledged),
-// 6 = 1 when this work-group stored Y (the last arriver under split-K), 7 = XCC id << 32 | HW_ID.
+// 6 = bit 0: this work-group stored Y (the last arriver under split-K); bits 1..: the latest
+// main-loop end over the work-group's waves (every wave posts its own to LDS), 7 = XCC id << 32 |
+// HW_ID.
 #ifdef BSG_TIMELINE
-#define BSG_TL_DECL uint64_t bsg_ts_[6] = {0, 0, 0, 0, 0, 0};
+#define BSG_TL_DECL                                        \
+  uint64_t bsg_ts_[6] = {0, 0, 0, 0, 0, 0};                \
+  __shared__ unsigned long long bsg_tl_last_;              \
+  if (threadIdx.x == 0) bsg_tl_last_ = 0;
 #define BSG_TL(i) (bsg_ts_[i] = wall_clock64())
 #define BSG_TL_IF(i, cond) \
   if (cond) bsg_ts_[i] = wall_clock64()
+#define BSG_TL_LOOP_END()                                                   \
+  do {                                                                      \
+    bsg_ts_[3] = wall_clock64();                                            \
+    if ((threadIdx.x & 63) == 0) atomicMax(&bsg_tl_last_, (unsigned long long)bsg_ts_[3]); \
+  } while (0)
 #define BSG_TL_END(p, stored_y)                                                                         \
   do {                                                                                                 \
     __builtin_amdgcn_s_waitcnt(0x0F70);                                                                \
     bsg_ts_[5] = wall_clock64();                                                                       \
+    __syncthreads();                                                                                   \
     if ((p).tl != nullptr && threadIdx.x == 0) {                                                       \
       uint64_t* t_ = (p).tl + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8;                      \
       for (int i_ = 0; i_ < 6; ++i_) t_[i_] = bsg_ts_[i_];                                             \
-      t_[6] = (stored_y) ? 1u : 0u;                                                                    \
+      t_[6] = ((stored_y) ? 1u : 0u) | ((uint64_t)bsg_tl_last_ << 1);                                  \
       t_[7] = ((uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |                          \
               (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);                                     \
     }                                                                                                  \
@@ -103,6 +114,7 @@ constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, 
 #define BSG_TL_DECL
 #define BSG_TL(i) ((void)0)
 #define BSG_TL_IF(i, cond) ((void)0)
+#define BSG_TL_LOOP_END() ((void)0)
 #define BSG_TL_END(p, stored_y) ((void)0)
 #endif
 
@@ -644,7 +656,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
       BSG_TL_IF(2, u0 + d == pad);
     }
   }
-  BSG_TL(3);
+  BSG_TL_LOOP_END();
 
   const size_t tile_lin = (size_t)blockIdx.y * (size_t)p.n_tiles + (size_t)tile;
   auto emit = [&](int f, f32x4 v) {
@@ -816,7 +828,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
       BSG_TL_IF(2, u0 + d == pad);
     }
   }
-  BSG_TL(3);
+  BSG_TL_LOOP_END();
 
   if constexpr (WK > 1) {
     // The second channel half hands its accumulators to the first through LDS.
@@ -1007,7 +1019,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
     }
   }
 
-  BSG_TL(3);
+  BSG_TL_LOOP_END();
   // Column c of subtile s: the quad of lanes 4c .. 4c+3 holds its four channel groups; two DPP
   // quad permutes (swap neighbours, then swap pairs) leave the column's sum on every lane of the
   // quad, (g0 + g1) + (g2 + g3) in a fixed order.
@@ -1172,7 +1184,7 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
       BSG_TL_IF(2, u0 + d == pad);
     }
   }
-  BSG_TL(3);
+  BSG_TL_LOOP_END();
 
   // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read: s_red is separate).
 #pragma unroll
