@@ -17,6 +17,10 @@ const KernelEntry kEntries[] = {
     // kind 6: every wave both channel halves, waves split the blocks
     BSG_V1(1, 3, 2, 4), BSG_V1(1, 3, 4, 4), BSG_V1(2, 3, 2, 4), BSG_V1(2, 3, 4, 2), BSG_V1(4, 3, 2, 2),
     BSG_V1(4, 3, 4, 2), BSG_V1(4, 2, 4, 2), BSG_V1(4, 3, 2, 4), BSG_V1(1, 1, 4, 4), BSG_V1(1, 2, 4, 4),
+    // more loads in flight per compute unit for short slices (a slice costs one round of loads
+    // per `depth` blocks): 8 block-slice waves, or depth 8
+    BSG_V1(1, 1, 8, 4), BSG_V1(1, 1, 4, 8), BSG_V1(1, 2, 8, 4), BSG_V1(1, 2, 4, 8), BSG_V1(2, 1, 4, 4),
+    BSG_V1(2, 2, 4, 4), BSG_V1(2, 1, 8, 4),
 };
 }  // namespace
 
