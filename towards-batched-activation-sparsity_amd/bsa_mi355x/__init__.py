@@ -8,6 +8,7 @@ layer that mirrors the reference's Python entry points
 (kernels/shared_mask_batched_triton_min_runtime.py).
 """
 from ._lib import BLOCK_K, MAX_NBLK, BsgArgError, BsgDtypeError, BsgError, BsgUnsupported, Plan, load
+from .autotune import set_autotune
 from .runtime import (INDEX_BLOCK_META_SIZE, TileConfig, _build_active_k_bitmap, _get_prepacked_weight_block_major,
                       _prepacked_block_sparse_gemm_from_active_blocks,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload,
@@ -27,7 +28,7 @@ from .sparse2d import (INDEX_BLOCK_OUT_META_SIZE, _get_cached_active_n_blocks_de
 
 __all__ = [
     "BLOCK_K", "MAX_NBLK", "INDEX_BLOCK_META_SIZE", "Plan", "TileConfig", "load",
-    "BsgError", "BsgArgError", "BsgDtypeError", "BsgUnsupported",
+    "BsgError", "BsgArgError", "BsgDtypeError", "BsgUnsupported", "set_autotune",
     "_build_active_k_bitmap", "_get_prepacked_weight_block_major", "_sort_active_blocks_asc",
     "_prepacked_block_sparse_gemm_from_active_blocks",
     "_prepacked_block_sparse_gemm_from_active_blocks_splitk",

@@ -225,7 +225,9 @@ def _workspace(prefix: str, device: torch.device, nbytes: int, layout: tuple = (
 
 class _KernelHandle:
     """Stands in for a Triton autotuned kernel object: `best_config` reports the tile of the
-    last launch (scripts/profile_kernel_configs.py:135 reads it)."""
+    last launch (scripts/profile_kernel_configs.py:135 reads it): the tuned table's plan for a
+    tabulated problem, the first-call tuned winner for any other key (bsa_mi355x.autotune), or
+    the explicit plan the call named."""
 
     def __init__(self, name: str):
         self.__name__ = name
@@ -331,36 +333,90 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
     else:
         mode = "dense"
         na_for_plan = nblk
-    pl = resolve_plan(bt, n_dim, nblk, na_for_plan, dev, plan, dense=(mode == "dense"))
+    if mode == "list":
+        if active_blocks.dtype != torch.int32:
+            active_blocks = active_blocks.to(torch.int32)
+        active_blocks = active_blocks.contiguous()
+    elif mode == "bitmap":
+        if bitmap.dtype not in (torch.uint8, torch.bool, torch.int8):
+            raise TypeError(f"bitmap must be uint8, got {bitmap.dtype}")
+        bitmap = bitmap.contiguous()
+        if bitmap.numel() < nbm or bitmap.device != dev:
+            raise ValueError(f"bitmap must hold total_k_blocks={nbm} entries on {dev}")
+    kd = x2d.shape[1]
+
+    def launch(pl: Plan, ws_ptr, ws_bytes: int) -> int:
+        with torch.cuda.device(dev):
+            if mode == "list":
+                nad = num_active_dev.data_ptr() if num_active_dev is not None else None
+                return lib.bsg_gemm(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
+                                    active_blocks.data_ptr() if na > 0 else None, na, nad, y2d.data_ptr(),
+                                    y2d.stride(0), code, ws_ptr, ws_bytes, ctypes_byref(pl), stream)
+            if mode == "bitmap":
+                return lib.bsg_gemm_bitmap(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
+                                           bitmap.data_ptr(), nbm, y2d.data_ptr(), y2d.stride(0), code, ws_ptr,
+                                           ws_bytes, ctypes_byref(pl), stream)
+            return lib.bsg_gemm_dense(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
+                                      y2d.data_ptr(), y2d.stride(0), code, ws_ptr, ws_bytes, ctypes_byref(pl), stream)
+
+    pl = None
+    if plan is None or not any(plan.as_tuple()):
+        pl = _first_call_plan(bt, n_dim, nblk, na_for_plan, mode, code, dev, _tuning_launcher(lib, bt, n_dim, dev, launch))
+    if pl is None:
+        pl = resolve_plan(bt, n_dim, nblk, na_for_plan, dev, plan, dense=(mode == "dense"))
     ws_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
     ws_ptr = (_workspace(workspace_prefix, dev, ws_bytes, (bt, n_dim) + pl.as_tuple()).data_ptr()
               if ws_bytes > 0 else None)
-    kd = x2d.shape[1]
-    with torch.cuda.device(dev):
-        if mode == "list":
-            if active_blocks.dtype != torch.int32:
-                active_blocks = active_blocks.to(torch.int32)
-            active_blocks = active_blocks.contiguous()
-            nad = num_active_dev.data_ptr() if num_active_dev is not None else None
-            rc = lib.bsg_gemm(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
-                              active_blocks.data_ptr() if na > 0 else None, na, nad, y2d.data_ptr(),
-                              y2d.stride(0), code, ws_ptr, ws_bytes, ctypes_byref(pl), stream)
-        elif mode == "bitmap":
-            if bitmap.dtype not in (torch.uint8, torch.bool, torch.int8):
-                raise TypeError(f"bitmap must be uint8, got {bitmap.dtype}")
-            bitmap = bitmap.contiguous()
-            if bitmap.numel() < nbm or bitmap.device != dev:
-                raise ValueError(f"bitmap must hold total_k_blocks={nbm} entries on {dev}")
-            rc = lib.bsg_gemm_bitmap(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
-                                     bitmap.data_ptr(), nbm, y2d.data_ptr(), y2d.stride(0), code, ws_ptr, ws_bytes,
-                                     ctypes_byref(pl), stream)
-        else:
-            rc = lib.bsg_gemm_dense(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim, y2d.data_ptr(),
-                                    y2d.stride(0), code, ws_ptr, ws_bytes, ctypes_byref(pl), stream)
-    check(rc)
+    check(launch(pl, ws_ptr, ws_bytes))
     if kernel is not None:
         kernel.last_plan = pl
     return pl
+
+
+def _tuning_launcher(lib, bt: int, n_dim: int, dev: torch.device, launch):
+    """launch(plan) for first-call tuning: one scratch workspace (grown as candidates need, freed
+    with the closure), its counters cleared whenever the candidate changes, since the previous
+    candidate's partials may lie where this one's counters start."""
+    state = {"buf": None, "last": None}
+
+    def run(pl: Plan) -> int:
+        need = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
+        if need < 0:
+            return need
+        if need == 0:
+            return launch(pl, None, 0)
+        buf = state["buf"]
+        if buf is None or buf.numel() < need:
+            buf = state["buf"] = torch.zeros(need, dtype=torch.uint8, device=dev)
+            state["last"] = pl.as_tuple()
+        elif state["last"] != pl.as_tuple():
+            rc = lib.bsg_workspace_init(buf.data_ptr(), buf.numel(), _stream_handle(dev))
+            if rc != _lib.BSG_OK:
+                return rc
+            state["last"] = pl.as_tuple()
+        return launch(pl, buf.data_ptr(), buf.numel())
+
+    return run
+
+
+def _first_call_plan(bt: int, n_dim: int, nblk: int, na: int, mode: str, code: int, dev: torch.device,
+                     launch) -> Optional[Plan]:
+    """For a problem the tuned table does not cover: the plan first-call tuning chose for its key
+    (tuned now, on this call's buffers, unless a stream is being captured or tuning is off), or
+    None (table plan or library heuristics)."""
+    from . import autotune, tuning
+
+    if tuning.lookup(bt, n_dim, nblk, na, dense=(mode == "dense")) is not None:
+        return None
+    k = autotune.key(n_dim, nblk, bt, na, mode, code)
+    pl = autotune.cached(k)
+    if pl is not None or not autotune.enabled() or torch.cuda.is_current_stream_capturing():
+        return pl
+    cands = tuning.candidate_plans(bt, na, nblk)
+    heuristic = resolve_plan(bt, n_dim, nblk, na, dev, None, dense=(mode == "dense"), lookup_plan=False)
+    if heuristic.as_tuple() not in {c.as_tuple() for c in cands}:
+        cands.append(heuristic)
+    return autotune.tune(k, cands, launch, dev)
 
 
 def _sort_active_blocks_asc(active_blocks: torch.Tensor) -> torch.Tensor:
