@@ -21,6 +21,8 @@ const KernelEntry kEntries[] = {
     // per `depth` blocks): 8 block-slice waves, or depth 8
     BSG_V1(1, 1, 8, 4), BSG_V1(1, 1, 4, 8), BSG_V1(1, 2, 8, 4), BSG_V1(1, 2, 4, 8), BSG_V1(2, 1, 4, 4),
     BSG_V1(2, 2, 4, 4), BSG_V1(2, 1, 8, 4),
+    // 6-subtile groups at 64 rows (N = 22016 over 256 compute units)
+    BSG_V1(4, 6, 2, 2), BSG_V1(4, 6, 4, 2),
 };
 }  // namespace
 
