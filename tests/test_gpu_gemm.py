@@ -221,6 +221,14 @@ def test_pack_layout_bit_exact(dev):
         assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), (n, k)
         got_kn = bsa.pack_weight(to_dev(np.ascontiguousarray(w_nk.T), dev), layout="kn").cpu().numpy()
         assert np.array_equal(got_kn.view(np.uint16), want.view(np.uint16)), (n, k, "kn")
+        # the reference-named accessor: the cached tiled tensor, guarded against reference-layout
+        # slicing, and its block_major() view equal to the reference packing bit for bit
+        tp = bsa._get_prepacked_weight_block_major(to_dev(w_nk, dev), 64, cache_prefix="packacc")
+        assert isinstance(tp, bsa.TiledPackedWeight) and tuple(tp.shape) == want.shape
+        with pytest.raises(TypeError):
+            tp[0]
+        bm = tp.block_major(n).cpu().numpy()
+        assert np.array_equal(bm.view(np.uint16), orc.pack_kmajor(w_nk).view(np.uint16)), (n, k, "block_major")
 
 
 @pytest.mark.parametrize("plan", [(8, 16, 2, 4, 16, 1), (8, 16, 4, 4, 16, 2), (8, 16, 8, 4, 64, 4), (8, 32, 8, 4, 64, 4)])

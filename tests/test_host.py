@@ -236,3 +236,23 @@ def test_reference_prior_length_rule_on_the_host():
     p = torch.ones(64)
     assert _prior_or_none(p, x) is p
     assert _prior_or_none(None, x) is None
+
+
+def test_tiled_packed_weight_block_major_matches_the_reference_packing():
+    """TiledPackedWeight (what _get_prepacked_weight_block_major returns) undoes the tile order
+    exactly: block_major(N) of tile_permute(pack_kmajor(W)) is pack_kmajor(W) (KRN:3152-3162),
+    including a K tail and an N that is not a multiple of 16; reference-layout indexing raises."""
+    import numpy as np
+    import torch
+
+    from oracle import bsg_oracle as orc
+    from bsa_mi355x.runtime import TiledPackedWeight
+
+    for n, k in ((100, 1000), (48, 64), (37, 200)):
+        w = np.random.default_rng(n * k).normal(0, 0.02, size=(n, k)).astype(np.float16)
+        ref = orc.pack_kmajor(w)
+        tp = torch.from_numpy(orc.tile_permute(ref)).as_subclass(TiledPackedWeight)
+        assert np.array_equal(tp.block_major(n).numpy().view(np.uint16), ref.view(np.uint16)), (n, k)
+        with pytest.raises(TypeError):
+            tp[0, :, :n]
+        assert "TiledPackedWeight" in repr(tp)

@@ -9,7 +9,7 @@ layer that mirrors the reference's Python entry points
 """
 from ._lib import BLOCK_K, MAX_NBLK, BsgArgError, BsgDtypeError, BsgError, BsgUnsupported, Plan, load
 from .autotune import set_autotune
-from .runtime import (INDEX_BLOCK_META_SIZE, TileConfig, _build_active_k_bitmap, _get_prepacked_weight_block_major,
+from .runtime import (INDEX_BLOCK_META_SIZE, TiledPackedWeight, TileConfig, _build_active_k_bitmap, _get_prepacked_weight_block_major,
                       _prepacked_block_sparse_gemm_from_active_blocks,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload_splitk,
@@ -27,7 +27,7 @@ from .sparse2d import (INDEX_BLOCK_OUT_META_SIZE, _get_cached_active_n_blocks_de
                        gemm_2d_packed, nmask_blocks, scatter_nblocks)
 
 __all__ = [
-    "BLOCK_K", "MAX_NBLK", "INDEX_BLOCK_META_SIZE", "Plan", "TileConfig", "load",
+    "BLOCK_K", "MAX_NBLK", "INDEX_BLOCK_META_SIZE", "Plan", "TileConfig", "TiledPackedWeight", "load",
     "BsgError", "BsgArgError", "BsgDtypeError", "BsgUnsupported", "set_autotune",
     "_build_active_k_bitmap", "_get_prepacked_weight_block_major", "_sort_active_blocks_asc",
     "_prepacked_block_sparse_gemm_from_active_blocks",

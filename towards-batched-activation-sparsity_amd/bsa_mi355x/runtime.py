@@ -133,9 +133,35 @@ def _packed_entry(weight: torch.Tensor, block_k: int, cache_prefix: str) -> _Pac
     return entry
 
 
+class TiledPackedWeight(torch.Tensor):
+    """What `_get_prepacked_weight_block_major` returns: the cached packed weight, sharing its
+    storage, in this build's MFMA tile order [nblk, Np/16, 1024] (element (j, k, n) at
+    [j, n // 16, (k // 32) * 512 + ((k % 32) // 8) * 128 + (n % 16) * 8 + k % 8], Np = N
+    rounded up to 16), not the reference's [nblk, 64, N] (KRN:3162).  The reference's drivers
+    only call the function to warm the cache (BPS:160, PKC:116, RRD:321-324); code that sliced
+    the result as the reference layout would read the wrong elements, so Python indexing
+    raises.  `block_major(n)` returns the reference layout (a copy)."""
+
+    def __getitem__(self, item):
+        raise TypeError("the packed weight is in the MFMA tile order [nblk, Np/16, 1024], not [nblk, 64, N]; "
+                        "use .block_major(N) for the reference layout")
+
+    def block_major(self, n: int) -> torch.Tensor:
+        """The reference's [nblk, 64, n] block-major packing (KRN:3152-3162), as a new tensor."""
+        w = self.as_subclass(torch.Tensor)
+        nblk, t16, _ = w.shape
+        # [j, t, h, g, c, e] -> [j, h, g, e, t, c]: k = 32h + 8g + e, n = 16t + c
+        w6 = w.reshape(nblk, t16, 2, 4, 16, 8).permute(0, 2, 3, 5, 1, 4)
+        return w6.reshape(nblk, BLOCK_K, t16 * 16)[:, :, : int(n)].contiguous()
+
+    def __repr__(self) -> str:
+        return f"TiledPackedWeight(shape={tuple(self.shape)}, dtype={self.dtype}, device={self.device})"
+
+
 def _get_prepacked_weight_block_major(weight: torch.Tensor, block_k: int, cache_prefix: str = "gemm") -> torch.Tensor:
-    """Packed weight for nn.Linear `weight` [N, K], cached per prefix (KRN:3133-3163)."""
-    return _packed_entry(weight, block_k, cache_prefix).packed
+    """Packed weight for nn.Linear `weight` [N, K], cached per prefix (KRN:3133-3163), as a
+    TiledPackedWeight view of the cache entry."""
+    return _packed_entry(weight, block_k, cache_prefix).packed.as_subclass(TiledPackedWeight)
 
 
 def release_prepacked_weights(cache_prefix: Optional[str] = None) -> None:
