@@ -536,6 +536,7 @@ def run_matrix(args, dev):
     mf = load_mfma_util(focus)
     if mf is not None:
         roofline["mfma_util_counter"] = mf
+    roofline["by_kernel"] = kernel_shares(points, per)
     if not args.only:
         rd = read_calibration_us(fp)
         roofline["practical_read"] = {
@@ -591,6 +592,26 @@ def run_matrix(args, dev):
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def kernel_shares(points, per):
+    """Per kernel (symbol prefix of the plans' kinds): its share of one step's GPU time (each point
+    weighted by its launches per step), and active-weight bytes over that time against the peak."""
+    acc = {}
+    for p in points:
+        name = KERNEL_NAMES.get(p.plan.kind, "bsg_gemm")
+        us = per[p.name][1] * p.copies
+        a = acc.setdefault(name, {"us": 0.0, "bytes": 0, "points": []})
+        a["us"] += us
+        a["bytes"] += p.active_bytes * p.copies
+        a["points"].append(p.name)
+    total = sum(a["us"] for a in acc.values())
+    out = {}
+    for name, a in sorted(acc.items(), key=lambda kv: -kv[1]["us"]):
+        gbs = a["bytes"] / (a["us"] * 1e-6) / 1e9
+        out[name] = {"time_share": round(a["us"] / total, 4), "GBps": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "points": a["points"]}
+    return out
 
 
 def run_2d(args, dev):

@@ -256,3 +256,22 @@ def test_tiled_packed_weight_block_major_matches_the_reference_packing():
         with pytest.raises(TypeError):
             tp[0, :, :n]
         assert "TiledPackedWeight" in repr(tp)
+
+
+def test_bench_kernel_shares_weight_points_by_launches_per_step():
+    """roofline.by_kernel: each kernel's share of a step's time (a point's mean µs x its launches
+    per step) and its active bytes over that time."""
+    import types
+
+    bench = _bench_module()
+    P = types.SimpleNamespace
+    pts = [P(name="a", plan=P(kind=1), copies=10, active_bytes=1_000_000),
+           P(name="b", plan=P(kind=6), copies=5, active_bytes=4_000_000),
+           P(name="c", plan=P(kind=1), copies=2, active_bytes=9_000_000)]
+    per = {"a": (3.0, 3.0), "b": (10.0, 10.0), "c": (15.0, 15.0)}
+    out = bench.kernel_shares(pts, per)
+    assert list(out) == ["bsg_gemm_kernel", "bsg_gemm_vt_kernel"]  # 60 µs vs 50 µs per step
+    k1 = out["bsg_gemm_kernel"]
+    assert k1["points"] == ["a", "c"] and abs(k1["time_share"] - 60 / 110) < 1e-4
+    assert abs(k1["GBps"] - 28_000_000 / 60e-6 / 1e9) < 0.1
+    assert abs(out["bsg_gemm_vt_kernel"]["frac"] - (20_000_000 / 50e-6 / 1e9) / bench.HBM_PEAK_GBS) < 1e-4
