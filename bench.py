@@ -21,6 +21,12 @@ cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host
                configs[0] point, down_proj B=16 with 86 of 172 blocks; every point also carries
                its own CPU time
 
+The same line also carries, measured in the same run after the matrix (skip with --no-extras):
+fused_select_gemm = configs[3] (exact-L1 select k=31 of 64 + gate/up GEMM at B=64, indices
+checked bit-exact), decode_step = configs[4] (the 32-layer decode step of linears as one
+hipGraph), perstep_replay = the reference's headline table (its per-step sparsity maps of the
+224-GEMM decode step) at B=2, 4, 8, 16, 32, 64.
+
     python bench.py [--steps K] [--warmup W]
                     [--workload llama|down_sweep|fused|decode|perstep|2d] [--only POINT]
 """
@@ -83,6 +89,9 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=32, help="decode workload: number of layers")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="llama workload: skip the configs[3] / configs[4] / per-step replay measurements that "
+                         "the default line carries")
     ap.add_argument("--only", default=None, help="time only this point (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the GEMMs, replay a plain device copy of MIB MiB (PMC calibration)")
@@ -549,6 +558,36 @@ def run_matrix(args, dev):
             if p.dense and p.bt == 16:
                 row["torch_mm_us"] = round(torch_mm_us(p), 3)
                 log(f"torch.mm (hipBLASLt) on {p.name}: {row['torch_mm_us']:.2f} us")
+    extras = {}
+    if args.workload == "llama" and not args.only and not args.no_extras:
+        # BASELINE configs[3] and configs[4] and the reference's headline table, measured in the
+        # same run; the matrix's weight pools and graphs are released first
+        for p in points:
+            p.graph = None
+        step_graph = None
+        for pool in pools.values():  # the CPU baseline below needs only the pools' host copies
+            pool.packed = []
+            pool._kn = None
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        log("configs[3]: fused exact-L1 select + GEMM ...")
+        extras["fused_select_gemm"] = measure_fused(args, dev)
+        log(f"configs[3] done ({time.perf_counter() - t0:.1f} s): {extras['fused_select_gemm']['us_select_plus_gemm']} us")
+        log("configs[4]: 32-layer decode step ...")
+        extras["decode_step"] = measure_decode(args, dev)
+        log(f"configs[4] done ({time.perf_counter() - t0:.1f} s): {extras['decode_step']['ms_per_step']} ms/step")
+        log("per-step replay of the reference's sparsity maps at every batch size ...")
+        rows_ps, _, _ = measure_perstep(args, dev)
+        extras["perstep_replay"] = {
+            "workload": "the reference's headline table (scripts/bench_perstep_actual_kernel_speedup.py, "
+                        "README.md:32-36): its per-step sparsity maps of the 224-GEMM decode step replayed on this "
+                        "build at B=2..64; speedup of the sparse step over our own dense kernel and over "
+                        "hipBLASLt, beside the reference's A100X speedup over cuBLAS",
+            "rows": [{k: r[k] for k in ("B", "group_steps", "mean_sparsity", "speedup_vs_own_dense",
+                                        "speedup_vs_hipblaslt", "reference_a100x_speedup_vs_cublas",
+                                        "sparse_us_step_mean", "replay_tokens_per_s",
+                                        "reference_a100x_replay_tokens_per_s")} for r in rows_ps]}
+        log(f"extras done ({time.perf_counter() - t0:.1f} s)")
     cpu = None
     if not args.no_cpu and not args.only:
         log("cpu baseline ...")
@@ -591,6 +630,7 @@ def run_matrix(args, dev):
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    line.update(extras)
     print(json.dumps(line), flush=True)
 
 
@@ -690,10 +730,10 @@ def run_2d(args, dev):
     print(json.dumps(line), flush=True)
 
 
-def run_fused(args, dev):
+def measure_fused(args, dev):
     """fused exact-L1 selection (k=31 of 64) + sparse GEMM on gate/up at B=64
     (K=4096 -> N=11008), rotated over >= 1 GiB of distinct active weight; indices checked
-    bit-exact against the oracle first."""
+    bit-exact against the oracle first.  Returns the measured fields."""
     import numpy as np
     import torch
 
@@ -735,27 +775,39 @@ def run_fused(args, dev):
     t_gemm = _graph_time([gemm_only(i) for i in range(r)], reps)[0] / r
     t_sel = _graph_time([select_only(i) for i in range(r)], reps)[0] / r
     gbs = pt.active_bytes / (t_fused * 1e-6) / 1e9
+    out = {"workload": "fused exact-L1 select (k=31 of 64) + sparse GEMM, gate/up B=64 K=4096 N=11008 (configs[3])",
+           "us_select_plus_gemm": round(t_fused, 3), "us_gemm_only": round(t_gemm, 3),
+           "us_select_only": round(t_sel, 3), "select_overhead_us": round(t_fused - t_gemm, 3),
+           "GBps_active": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "plan": list(plan.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True}
+    del pool, pt
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_fused(args, dev):
+    """`--workload fused`: the configs[3] measurement as its own JSON line."""
+    f = measure_fused(args, dev)
+    r, reps = f["launches_per_replay"], f["replays"]
     line = {
-        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": reps,
-        "warmup": 2, "ms_per_step": round(t_fused * r / 1000.0, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp16",
+        "metric": METRIC, "value": f["GBps_active"], "unit": "GB/s", "n_gpus": 1, "steps": reps,
+        "warmup": 2, "ms_per_step": round(f["us_select_plus_gemm"] * r / 1000.0, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) [K,N], X~N(0,1); >=1 GiB of distinct active weight "
                 "per replay",
-        "config": {"workload": "fused exact-L1 select (k=31 of 64) + sparse GEMM, gate/up B=64 K=4096 N=11008 "
-                               "(configs[3])", "plan": list(plan.as_tuple()), "launches_per_replay": r},
-        "us_select_plus_gemm": round(t_fused, 3), "us_gemm_only": round(t_gemm, 3), "us_select_only": round(t_sel, 3),
-        "select_overhead_us": round(t_fused - t_gemm, 3),
-        "indices_bit_exact": True,
+        "config": {"workload": f["workload"], "plan": f["plan"], "launches_per_replay": r},
+        **{k: f[k] for k in ("us_select_plus_gemm", "us_gemm_only", "us_select_only", "select_overhead_us",
+                             "indices_bit_exact")},
     }
     print(json.dumps(line), flush=True)
 
 
-def run_decode(args, dev):
+def measure_decode(args, dev):
     """Llama-2-7B-shaped decode step of linears (layers x {qkv, o, gate/up,
     down}), B=64, per-projection masks from the fused selector at density 0.48 (k=31/64, 83/172),
     the whole step captured as one hipGraph.  Its full parity check (every projection's indices,
     first and last layer outputs, replay against eager) is tests/test_gpu_decode.py; here the
-    first and last layers are spot-checked before timing."""
+    first and last layers are spot-checked before timing.  Returns the measured fields."""
     import numpy as np
     import torch
 
@@ -799,18 +851,32 @@ def run_decode(args, dev):
     per = [a.elapsed_time(b) for a, b in ts]
     ms = total_ms / args.steps
     gbs = step.active_bytes / (ms * 1e-3) / 1e9
+    out = {"workload": f"Llama-2-7B decode step of linears, {args.layers} layers x (select + GEMM) x "
+                       "{qkv N=12288, o, gate/up N=22016, down}, B=64, density 0.48, one hipGraph (configs[4])",
+           "ms_per_step": round(ms, 4), "step_ms_median": round(statistics.median(per), 4),
+           "GBps_active": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": args.steps,
+           "warmup": args.warmup, "resident_weight_gb": round(step.resident_weight_bytes / 1e9, 3),
+           "active_gb_per_step": round(step.active_bytes / 1e9, 4),
+           "launches_per_step": len(step.layers) * len(step.layers[0]) * 2,
+           "floor_ms_at_8TBps": round(step.active_bytes / 8e12 * 1e3, 4),
+           "parity": "indices bit-exact and outputs within tolerance on the first and last layers"}
+    del step
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_decode(args, dev):
+    """`--workload decode`: the configs[4] measurement as its own JSON line."""
+    d = measure_decode(args, dev)
     line = {
-        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": d["GBps_active"], "unit": "GB/s", "n_gpus": 1, "steps": d["steps"],
+        "warmup": d["warmup"], "ms_per_step": d["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: torch seed 1234 on device, W~N(0,0.02), X~N(0,1) (Laplace(0,0.05) for down)",
-        "config": {"workload": f"Llama-2-7B decode step of linears, {args.layers} layers x (select + GEMM) x "
-                               "{qkv N=12288, o, gate/up N=22016, down}, B=64, density 0.48, one hipGraph (configs[4])",
-                   "resident_weight_gb": round(step.resident_weight_bytes / 1e9, 3),
-                   "active_gb_per_step": round(step.active_bytes / 1e9, 4),
-                   "launches_per_step": len(step.layers) * len(step.layers[0]) * 2},
-        "step_ms_median": round(statistics.median(per), 4),
-        "floor_ms_at_8TBps": round(step.active_bytes / 8e12 * 1e3, 4),
+        "config": {"workload": d["workload"], "resident_weight_gb": d["resident_weight_gb"],
+                   "active_gb_per_step": d["active_gb_per_step"], "launches_per_step": d["launches_per_step"]},
+        "step_ms_median": d["step_ms_median"],
+        "floor_ms_at_8TBps": d["floor_ms_at_8TBps"],
     }
     print(json.dumps(line), flush=True)
 
@@ -818,7 +884,7 @@ def run_decode(args, dev):
 PERSTEP_FIXTURE = os.path.join(ROOT, "tests", "golden", "perstep_smaps.npz")
 
 
-def run_perstep(args, dev):
+def measure_perstep(args, dev, batches=None):
     """Oracle-map replay (the reference's headline benchmark,
     scripts/bench_perstep_actual_kernel_speedup.py): for each batch size, every group-step's
     S-map of 7 projections x 32 layers (tests/golden/perstep_smaps.npz, from the reference's
@@ -828,7 +894,8 @@ def run_perstep(args, dev):
     BPS:148-172) with this build's sparse kernel, its dense variant and hipBLASLt (torch.mm),
     every one rotated over >= 1 GiB of distinct active weight; a step's speedup is
     sum(dense) / sum(sparse) over its 224 GEMMs, averaged over the 55 group-steps of a batch
-    size, next to the reference's A100X numbers for the same maps."""
+    size, next to the reference's A100X numbers for the same maps.  Returns (rows per batch size,
+    active bytes and µs summed over the timed sparse cases)."""
     import numpy as np
     import torch
 
@@ -837,7 +904,8 @@ def run_perstep(args, dev):
     from oracle import bsg_oracle as orc
 
     fx = replay.load_maps(PERSTEP_FIXTURE)
-    batches = [int(b) for b in (args.batches.split(",") if args.batches else fx["ref_batch"])]
+    if batches is None:
+        batches = [int(b) for b in (args.batches.split(",") if args.batches else fx["ref_batch"])]
     cases_by_b = replay.cases_for_batches(fx, batches)
     need = {}
     for cases in cases_by_b.values():
@@ -925,6 +993,16 @@ def run_perstep(args, dev):
                                                        "throughput_speedup": round(ref_dense_ms / ref_sparse_ms, 3)}}
         results.append(row)
         log(json.dumps(row))
+    del pools
+    torch.cuda.empty_cache()
+    return results, total_bytes, total_us
+
+
+def run_perstep(args, dev):
+    """`--workload perstep`: the reference's headline table (every batch size) as one JSON line."""
+    results, total_bytes, total_us = measure_perstep(args, dev)
+    batches = [r["B"] for r in results]
+    reps = max(3, min(args.steps, 10))
     line = {
         "metric": METRIC, "value": round(total_bytes / (total_us * 1e-6) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": reps, "warmup": 2, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",

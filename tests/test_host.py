@@ -223,6 +223,22 @@ def test_bench_default_measures_configs2_with_active_byte_rotation():
     assert set(bench.KERNEL_NAMES) == {1, 2, 3, 4, 5, 6}
 
 
+def test_bench_default_line_carries_configs3_configs4_and_the_perstep_table(monkeypatch):
+    """With no flags, bench.py runs the llama matrix and, in the same run, the fused select +
+    GEMM, the 32-layer decode step and the per-step replay at every batch
+    size of the reference's fixture; --no-extras and --only skip them."""
+    bench = _bench_module()
+    monkeypatch.setattr("sys.argv", ["bench.py"])
+    a = bench.parse_args()
+    assert (a.workload, a.gpus, a.no_extras, a.only, a.layers) == ("llama", 1, False, None, 32)
+    monkeypatch.setattr("sys.argv", ["bench.py", "--no-extras"])
+    assert bench.parse_args().no_extras
+    from bsa_mi355x import replay
+
+    fx = replay.load_maps(bench.PERSTEP_FIXTURE)
+    assert sorted(int(b) for b in fx["ref_batch"]) == [2, 4, 8, 16, 32, 64]
+
+
 def test_reference_prior_length_rule_on_the_host():
     """The drop-in selectors pass a block prior on only when it holds floor(K/64) entries
     (RRD:110-112): shorter and longer priors are dropped before any device call."""
