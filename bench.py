@@ -304,6 +304,30 @@ def cpu_baseline(point, seconds):
     }
 
 
+def cpu_select_gemm_us(x_np, w_kn_np, keep, runs=3):
+    """The CPU path of a select + GEMM (the oracle's exact-L1 top-k, then torch CPU gather + fp32
+    matmul, every host core): the median of a few runs after one warm-up."""
+    import torch
+
+    from oracle import bsg_oracle as orc
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    x = torch.from_numpy(x_np)
+    w = torch.from_numpy(w_kn_np)
+
+    def run():
+        idx = torch.from_numpy(orc.select_topk_l1(x_np, keep).astype("int64"))
+        return orc.gemm_ref_torch(x, w, idx)
+
+    run()
+    samples = []
+    for _ in range(runs):
+        t = time.perf_counter_ns()
+        run()
+        samples.append((time.perf_counter_ns() - t) / 1e3)
+    return statistics.median(samples)
+
+
 def cpu_point_us(point, runs=5):
     """The same op on the oracle's CPU path (torch CPU gather + fp32 matmul, every host core): the
     median of a few runs after one warm-up, shown beside each point's GPU time."""
@@ -775,11 +799,17 @@ def measure_fused(args, dev):
     t_gemm = _graph_time([gemm_only(i) for i in range(r)], reps)[0] / r
     t_sel = _graph_time([select_only(i) for i in range(r)], reps)[0] / r
     gbs = pt.active_bytes / (t_fused * 1e-6) / 1e9
+    cpu = {}
+    if not args.no_cpu:
+        cpu_us = cpu_select_gemm_us(pt.x_np, pool.w_kn_np, keep)
+        cpu = {"cpu_us_select_plus_gemm": round(cpu_us, 1), "cpu_cores": len(os.sched_getaffinity(0)),
+               "gpu_speedup_over_cpu": round(cpu_us / t_fused, 1)}
     out = {"workload": "fused exact-L1 select (k=31 of 64) + sparse GEMM, gate/up B=64 K=4096 N=11008 (configs[3])",
            "us_select_plus_gemm": round(t_fused, 3), "us_gemm_only": round(t_gemm, 3),
            "us_select_only": round(t_sel, 3), "select_overhead_us": round(t_fused - t_gemm, 3),
            "GBps_active": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-           "plan": list(plan.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True}
+           "plan": list(plan.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True,
+           **cpu}
     del pool, pt
     torch.cuda.empty_cache()
     return out
@@ -820,6 +850,7 @@ def measure_decode(args, dev):
         f"{step.active_bytes / 1e9:.3f} GB active per step ({time.perf_counter() - t0:.1f} s to build)")
     step.capture()
     torch.cuda.synchronize()
+    cpu_layer_us = 0.0
     for li in sorted({0, args.layers - 1}):
         for p in step.layers[li]:
             x = p.x.cpu().numpy()
@@ -827,9 +858,11 @@ def measure_decode(args, dev):
             got = p.idx[: min(p.keep, p.nblk)].cpu().numpy()
             if not np.array_equal(got, want):
                 raise SystemExit(f"decode layer {li} {p.name}: selected blocks differ from the oracle")
-            w_nk = orc.tile_unpermute(p.packed.cpu().numpy(), p.n).reshape(-1, p.n)[: p.k].T
-            if not orc.within_tolerance(p.y.float().cpu().numpy(), orc.gemm_ref(x, np.ascontiguousarray(w_nk), want)):
+            w_kn = np.ascontiguousarray(orc.tile_unpermute(p.packed.cpu().numpy(), p.n).reshape(-1, p.n)[: p.k])
+            if not orc.within_tolerance(p.y.float().cpu().numpy(), orc.gemm_ref(x, np.ascontiguousarray(w_kn.T), want)):
                 raise SystemExit(f"decode layer {li} {p.name}: output outside tolerance")
+            if li == 0 and not args.no_cpu:
+                cpu_layer_us += cpu_select_gemm_us(x, w_kn, p.keep, runs=1)
     log("decode: parity ok (first/last layer, all projections)")
     for _ in range(args.warmup):
         step.replay()
@@ -860,6 +893,12 @@ def measure_decode(args, dev):
            "launches_per_step": len(step.layers) * len(step.layers[0]) * 2,
            "floor_ms_at_8TBps": round(step.active_bytes / 8e12 * 1e3, 4),
            "parity": "indices bit-exact and outputs within tolerance on the first and last layers"}
+    if not args.no_cpu:
+        cpu_ms = cpu_layer_us * args.layers / 1e3
+        out.update({"cpu_ms_per_step": round(cpu_ms, 1), "cpu_cores": len(os.sched_getaffinity(0)),
+                    "cpu_sample": "layer 0's four select + GEMM on the oracle CPU path (exact-L1 top-k, torch CPU "
+                                  "gather + fp32 matmul), one run after a warm-up each, times the layer count",
+                    "gpu_speedup_over_cpu": round(cpu_ms / ms, 1)})
     del step
     torch.cuda.empty_cache()
     return out
