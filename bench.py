@@ -611,6 +611,8 @@ def run_matrix(args, dev):
                                         "speedup_vs_hipblaslt", "reference_a100x_speedup_vs_cublas",
                                         "sparse_us_step_mean", "replay_tokens_per_s",
                                         "reference_a100x_replay_tokens_per_s")} for r in rows_ps]}
+        log("each group-step as one 224-GEMM graph ...")
+        extras["perstep_replay"]["step_graphs"] = measure_step_graphs(args, dev)
         log(f"extras done ({time.perf_counter() - t0:.1f} s)")
     cpu = None
     if not args.no_cpu and not args.only:
@@ -1037,9 +1039,92 @@ def measure_perstep(args, dev, batches=None):
     return results, total_bytes, total_us
 
 
+def measure_step_graphs(args, dev, steps_per_batch=0):
+    """Each group-step of the reference's maps (tests/golden/perstep_smaps.npz) as one captured
+    graph of its 224 GEMMs (bsa_mi355x.replay.StepGraphs: 32 layers x q, k, v, o, gate, up,
+    down, ~13 GB of per-layer weights), against the dense step graph of the same batch size;
+    the step speedup is dense step time over sparse step time, beside the reference's A100X
+    speedup for the same group-step.  Layers 0 and 31 of each batch size's first group-step are
+    checked against the oracle before timing.  steps_per_batch 0: every group-step."""
+    import numpy as np
+    import torch
+
+    from bsa_mi355x import replay
+    from oracle import bsg_oracle as orc
+
+    fx = replay.load_maps(PERSTEP_FIXTURE)
+    t0 = time.perf_counter()
+    sg = replay.StepGraphs(dev)
+    log(f"step graphs: {sg.resident_weight_bytes / 1e9:.2f} GB of packed weights ({time.perf_counter() - t0:.1f} s)")
+    reps = 5
+    w_host = {}
+
+    def graph_ms(g):
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return statistics.median(ts)
+
+    rows = []
+    for bt in [int(v) for v in fx["ref_batch"]]:
+        sel = replay.batch_rows(fx, bt)
+        if steps_per_batch:
+            sel = sel[:steps_per_batch]
+        sg.set_batch(bt)
+        g = sg.capture(None)
+        dense_ms = graph_ms(g)
+        del g
+        rng = np.random.default_rng(SEED + bt)
+        sparse_ms, speed, ref_speed, active = [], [], [], []
+        for i, r in enumerate(sel):
+            lists = sg.step_lists(fx["smap_tenths"][r], rng)
+            g = sg.capture(lists)
+            if i == 0:
+                for li in sorted({0, sg.n_layers - 1}):
+                    for pi, shape in enumerate(replay.PROJ_SHAPE):
+                        key = (li, pi)
+                        if key not in w_host:
+                            k, n = replay.SHAPES[shape]
+                            w_host[key] = np.ascontiguousarray(
+                                orc.tile_unpermute(sg.packed[li][pi].cpu().numpy(), n).reshape(-1, n)[:k].T)
+                        x = sg.x[shape].cpu().numpy()
+                        ref = orc.gemm_ref(x, w_host[key], lists[li][pi].cpu().numpy())
+                        if not orc.within_tolerance(sg.y[li][pi].float().cpu().numpy(), ref):
+                            raise SystemExit(f"step graph B={bt} layer {li} {replay.PROJ_SHAPE[pi]}#{pi}: "
+                                             "output outside tolerance")
+            ms = graph_ms(g)
+            del g
+            sparse_ms.append(ms)
+            speed.append(dense_ms / ms)
+            ref_speed.append(float(fx["ref_step_speedup"][r]))
+            active.append(sg.active_bytes(lists))
+        row = {"B": bt, "group_steps": len(sel), "mean_sparsity": round(float(fx["mean_sparsity"][sel].mean()), 4),
+               "dense_step_ms": round(dense_ms, 4), "sparse_step_ms_mean": round(float(np.mean(sparse_ms)), 4),
+               "speedup_vs_own_dense": round(float(np.mean(speed)), 3),
+               "reference_a100x_step_speedup_same_steps": round(float(np.mean(ref_speed)), 3),
+               "sparse_GBps_active": round(float(np.mean(active)) / (float(np.mean(sparse_ms)) * 1e-3) / 1e9, 1),
+               "dense_GBps": round(sg.active_bytes(None) / (dense_ms * 1e-3) / 1e9, 1),
+               "tokens_per_s_sparse": round(bt / (float(np.mean(sparse_ms)) * 1e-3), 1)}
+        rows.append(row)
+        log(f"step graph B={bt}: {json.dumps(row)}")
+    del sg
+    torch.cuda.empty_cache()
+    return rows
+
+
 def run_perstep(args, dev):
     """`--workload perstep`: the reference's headline table (every batch size) as one JSON line."""
     results, total_bytes, total_us = measure_perstep(args, dev)
+    graphs = measure_step_graphs(args, dev)
     batches = [r["B"] for r in results]
     reps = max(3, min(args.steps, 10))
     line = {
@@ -1053,6 +1138,7 @@ def run_perstep(args, dev):
                                "B in " + ",".join(map(str, batches)) + " (the reference's headline speedup table)",
                    "value_is": "active-weight bytes / time over every distinct timed sparse case"},
         "perstep": results,
+        "step_graphs": graphs,
     }
     print(json.dumps(line), flush=True)
 

@@ -63,3 +63,58 @@ def test_perstep_cases_match_oracle(dev, weights, bt):
             torch.cuda.synchronize()
             assert_close(y.float().cpu().numpy(), orc.gemm_ref(xs[name], w_nk, idx),
                          f"B={bt} {name} density {tenths / 10} na={na} plan={pl.as_tuple()}")
+
+
+@pytest.fixture(scope="module")
+def step_graphs(dev):
+    sg = replay.StepGraphs(dev)
+    yield sg
+    del sg
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("bt", [2, 16, 64])
+def test_step_graph_matches_eager_and_oracle(dev, step_graphs, bt):
+    """One group-step of the reference's maps as a single 224-GEMM graph (32 layers x q, k, v,
+    o, gate, up, down, per-layer weights): every output of three replays equals the eager step
+    bit for bit, and layers 0, 15 and 31 are within the BASELINE tolerance of the oracle; the
+    dense step graph likewise on layer 0."""
+    sg = step_graphs
+    fx = replay.load_maps(FIXTURE)
+    row = replay.batch_rows(fx, bt)[0]
+    sg.set_batch(bt)
+    lists = sg.step_lists(fx["smap_tenths"][row], np.random.default_rng(bt))
+    assert sg.active_bytes(lists) < sg.active_bytes(None)
+    sg.run(lists)
+    torch.cuda.synchronize()
+    eager = [[y.clone() for y in layer] for layer in sg.y]
+    for li in (0, 15, 31):
+        for pi, shape in enumerate(replay.PROJ_SHAPE):
+            k, n = replay.SHAPES[shape]
+            w_nk = np.ascontiguousarray(orc.tile_unpermute(sg.packed[li][pi].cpu().numpy(), n).reshape(-1, n)[:k].T)
+            x = sg.x[shape].cpu().numpy()
+            print(f"step graph B={bt} layer {li} proj {pi} na={lists[li][pi].numel()}", flush=True)
+            assert_close(sg.y[li][pi].float().cpu().numpy(), orc.gemm_ref(x, w_nk, lists[li][pi].cpu().numpy()),
+                         f"B={bt} layer {li} proj {pi}")
+    g = sg.capture(lists)
+    for r in range(3):
+        for layer in sg.y:
+            for y in layer:
+                y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for li in range(sg.n_layers):
+            for pi in range(len(replay.PROJ_SHAPE)):
+                assert torch.equal(sg.y[li][pi].view(torch.int16), eager[li][pi].view(torch.int16)), (r, li, pi)
+    del g
+    gd = sg.capture(None)
+    gd.replay()
+    torch.cuda.synchronize()
+    for pi, shape in enumerate(replay.PROJ_SHAPE):
+        k, n = replay.SHAPES[shape]
+        nb = replay.nblk_of(shape)
+        w_nk = np.ascontiguousarray(orc.tile_unpermute(sg.packed[0][pi].cpu().numpy(), n).reshape(-1, n)[:k].T)
+        assert_close(sg.y[0][pi].float().cpu().numpy(), orc.gemm_ref(sg.x[shape].cpu().numpy(), w_nk, np.arange(nb)),
+                     f"dense B={bt} layer 0 proj {pi}")
+    del gd

@@ -8,7 +8,8 @@ blocks (BPS:84-87, at least one).  Each distinct (shape, density) case is timed 
 group-step's kernel-level speedup is the sum of its 224 dense times over the sum of its 224
 sparse times (BPS:122-172, 210-293).  This module holds that bookkeeping; the timing lives in
 bench.py (--workload perstep) and the parity check in tests/test_gpu_replay.py, so both run the
-same cases.
+same cases.  StepGraphs also runs a group-step's 224 GEMMs as one captured graph, so the step is
+timed whole (launch intervals and cache state included) instead of as a sum of per-case times.
 """
 from __future__ import annotations
 
@@ -86,3 +87,105 @@ def cases_for_batches(fx: Dict[str, np.ndarray], batches: Sequence[int], steps_p
             rows = rows[:steps_per_batch]
         out[int(bt)] = unique_cases(fx["smap_tenths"][rows])
     return out
+
+
+class StepGraphs:
+    """The 224-GEMM decode step of one group-step's map as one hipGraph (SURVEY's oracle-map
+    replay "in one hipGraph"): 32 layers x the 7 projections in the reference's order (q, k, v,
+    o, gate, up, down; BPS:122-141), each layer with its own random-init weights (the Llama-2-7B
+    step's ~13 GB, more than the 256 MB Infinity Cache can hold, so no rotation is needed), each
+    GEMM with floor(density * nblk) random active blocks from the map entry (BPS:84-87).  The
+    dense step is the same 224 launches with every block active.  Inputs are one synthetic X per
+    projection shape and batch size (the reference's per-case x, BPS:148-160); every GEMM writes
+    its own Y.  The weights are built once; set_batch() switches X and Y to another batch size."""
+
+    N_LAYERS = 32
+
+    def __init__(self, device, n_layers: int = N_LAYERS, seed: int = 1234, dtype=None):
+        import torch
+
+        from .runtime import pack_weight
+
+        self.device, self.n_layers, self.seed = device, int(n_layers), int(seed)
+        self.dtype = dtype or torch.float16
+        g = torch.Generator(device=device).manual_seed(seed)
+        # packed[layer][projection index]
+        self.packed = []
+        for _ in range(self.n_layers):
+            row = []
+            for shape in PROJ_SHAPE:
+                k, n = SHAPES[shape]
+                w = (torch.randn(k, n, generator=g, device=device, dtype=torch.float32) * 0.02).to(self.dtype)
+                row.append(pack_weight(w, layout="kn"))
+                del w
+            self.packed.append(row)
+        torch.cuda.synchronize(device)
+        self.batch = 0
+
+    @property
+    def resident_weight_bytes(self) -> int:
+        return sum(p.numel() * p.element_size() for row in self.packed for p in row)
+
+    def set_batch(self, batch: int) -> None:
+        import torch
+
+        self.batch = int(batch)
+        g = torch.Generator(device=self.device).manual_seed(self.seed + self.batch)
+        self.x = {s: torch.randn(self.batch, k, generator=g, device=self.device).to(self.dtype)
+                  for s, (k, _) in SHAPES.items()}
+        self.y = [[torch.empty(self.batch, SHAPES[s][1], dtype=self.dtype, device=self.device) for s in PROJ_SHAPE]
+                  for _ in range(self.n_layers)]
+
+    def step_lists(self, m: np.ndarray, rng: np.random.Generator):
+        """Per (layer, projection) ascending int32 device lists for one map [7, 32] (sparsity
+        tenths), drawn from rng in layer-major order."""
+        import torch
+
+        out = []
+        for li in range(self.n_layers):
+            row = []
+            for pi, shape in enumerate(PROJ_SHAPE):
+                nb = nblk_of(shape)
+                na = active_count(density_tenths(m[pi][li]), nb)
+                row.append(torch.from_numpy(random_blocks(rng, nb, na)).to(self.device))
+            out.append(row)
+        return out
+
+    def active_bytes(self, lists=None) -> int:
+        """Active-weight bytes of one step (lists None: the dense step)."""
+        total = 0
+        for li in range(self.n_layers):
+            for pi, shape in enumerate(PROJ_SHAPE):
+                na = nblk_of(shape) if lists is None else int(lists[li][pi].numel())
+                total += na * BLOCK_K * SHAPES[shape][1] * 2
+        return total
+
+    def run(self, lists=None) -> None:
+        """Enqueue the step on the current stream: lists[layer][proj] (None: the dense step)."""
+        from .runtime import gemm_packed, resolve_plan
+
+        for li in range(self.n_layers):
+            for pi, shape in enumerate(PROJ_SHAPE):
+                _, n = SHAPES[shape]
+                nb = nblk_of(shape)
+                idx = None if lists is None else lists[li][pi]
+                na = nb if idx is None else int(idx.numel())
+                plan = resolve_plan(self.batch, n, nb, na, self.device, None, dense=idx is None)
+                gemm_packed(self.x[shape], self.packed[li][pi], n, idx, self.y[li][pi], plan=plan,
+                            workspace_prefix=f"stepgraph_{shape}_{pi}")
+
+    def capture(self, lists=None):
+        """Warm up (plans, workspaces) on a side stream, then capture the step as one graph."""
+        import torch
+
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            self.run(lists)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.run(lists)
+        torch.cuda.synchronize(self.device)
+        return graph
