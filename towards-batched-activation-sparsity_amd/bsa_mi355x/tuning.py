@@ -158,7 +158,8 @@ def candidate_plans(bt: int, na: int, nblk: int) -> List[Plan]:
                 out.append(Plan(1, cols, waves, depth, rows, kind))
             continue
         if kind >= 5:  # variable-width column groups: the chip is filled without split-K
-            if rows == rb:
+            # 32- and 64-row batches also try two row groups of half the rows (as below)
+            if rows == rb or (rb >= 32 and rows == rb // 2):
                 out.append(Plan(1, cols, waves, depth, rows, kind))
             continue
         # 32-row batches also try 64-row tiles; 32- and 64-row batches also try two row groups of

@@ -23,6 +23,9 @@ const KernelEntry kEntries[] = {
     BSG_V1(2, 2, 4, 4), BSG_V1(2, 1, 8, 4),
     // 6-subtile groups at 64 rows (N = 22016 over 256 compute units)
     BSG_V1(4, 6, 2, 2), BSG_V1(4, 6, 4, 2),
+    // 32-row groups for 64-row batches (two row groups per column group; the second read of each
+    // weight line is an L2 hit on the same XCD): more block-slice waves and prefetch depth
+    BSG_V1(2, 2, 8, 4), BSG_V1(2, 2, 4, 8), BSG_V1(2, 3, 4, 4), BSG_V1(2, 4, 4, 4), BSG_V1(2, 4, 2, 4),
 };
 }  // namespace
 
