@@ -92,6 +92,7 @@ def _fused(dev, x, w_nk, k, plan=None):
     (64, 4096, 11008, 31, (1, 16, 8, 4, 64, 4)),  # channel-half waves; ranked in the GEMM
     (64, 4096, 4096, 31, (2, 16, 4, 4, 64, 2)),   # X tile in LDS, split-K 2; in the GEMM
     (64, 11008, 4096, 83, (4, 16, 8, 4, 64, 4)),  # 172 blocks over 8 waves; in the GEMM
+    (64, 11008, 4096, 83, (4, 16, 4, 4, 64, 2)),  # 172 blocks over 4 waves (9 rank items each); in the GEMM
     (16, 4096, 4096, 23, (1, 16, 1, 4, 16, 1)),   # one wave ranks 64 blocks; in the GEMM
     (16, 11008, 4096, 86, (1, 16, 2, 4, 16, 1)),  # 172 blocks, 2 waves: rank launch, then the list
     (2, 4096, 4096, 13, (1, 16, 4, 4, 2, 3)),     # dot-product kernel; in the GEMM

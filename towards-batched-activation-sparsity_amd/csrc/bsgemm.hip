@@ -38,6 +38,12 @@
 #include "bsg_device.hpp"
 #include "bsgemm.h"
 
+// The GEMM ranks the block scores itself (MODE_TOPK) when each of its waves has at most this many
+// rank items (64 blocks x 16 scores each); otherwise a separate rank launch runs first.
+#ifndef BSG_TOPK_ITEMS_PER_WAVE
+#define BSG_TOPK_ITEMS_PER_WAVE 12
+#endif
+
 #define BSG_VERSION_STR "bsgemm 0.1 (gfx950, mfma_f32_16x16x32)"
 
 namespace {
@@ -1155,10 +1161,12 @@ static int select_gemm_run(const void* x, int64_t ldx, int64_t bt, int64_t K, in
                 (long long)gws_bytes, (long long)need, pl.split_k);
   }
   // The GEMM ranks the scores itself when every work-group can do it quickly: the nblk^2
-  // compares, in items of 64 blocks x 16 scores, come to at most 8 items per wave.  Otherwise a
+  // compares, in items of 64 blocks x 16 scores, come to at most BSG_TOPK_ITEMS_PER_WAVE items per
+  // wave (12: down's 172 blocks on a four-wave plan take 9, 2.49 vs 2.51 ms per decode step with
+  // the rank launch that 8 forced).  Otherwise a
   // one-work-group rank launch (about 3 us) is cheaper than ranking in each work-group.
   const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
-  if (nblk <= BSG_TOPK_MAX_NBLK && items <= 8 * (int64_t)pl.waves_per_group) {
+  if (nblk <= BSG_TOPK_MAX_NBLK && items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group) {
     // Two launches: the block scores, then the GEMM, whose work-groups each rank them and walk
     // the kept list (work-group (0, 0) also publishes it).
     rc = select_l1_run(x, ldx, bt, K, k, idx_out, na_out, dtype, scores, stream, false);
