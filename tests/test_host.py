@@ -61,10 +61,12 @@ class _ScriptedCase:
     def __init__(self, times):
         self.times = {k: list(v) for k, v in times.items()}
         self.calls = []
+        self.selects = []
 
-    def time(self, plan, dense=False):
+    def time(self, plan, dense=False, select=False):
         key = plan.as_tuple()
         self.calls.append(key)
+        self.selects.append(select)
         v = self.times[key].pop(0)
         if v is None:
             raise bsa.BsgUnsupported(-5, "not instantiated")
@@ -85,6 +87,32 @@ def test_tuner_retimes_close_candidates():
     case = _ScriptedCase({a.as_tuple(): [5.0], c.as_tuple(): [6.0]})
     assert tuning._pick(case, [a, c]) == (5.0, a)
     assert tuning._pick(_ScriptedCase({d.as_tuple(): [None]}), [d]) == (float("inf"), None)
+    # the selection + GEMM tuning times every candidate through the select path
+    case = _ScriptedCase({a.as_tuple(): [5.0, 4.8, 4.9, 4.85], b.as_tuple(): [4.9, 5.6, 5.5, 5.7]})
+    tuning._pick(case, [a, b], select=True)
+    assert case.selects and all(case.selects)
+
+
+def test_lookup_prefers_select_entries_for_select_gemm(tmp_path):
+    """Entries timed as selection + GEMM ("select": true) answer select lookups first and never
+    plain-GEMM lookups; a select lookup with no select entry in its row bucket falls back to the
+    plain GEMM's entries."""
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps({"entries": [
+        {"bt": 64, "N": 4096, "K": 11008, "na": 86, "dense": False, "plan": [4, 16, 4, 4, 64, 2], "us": 1.0},
+        {"bt": 64, "N": 4096, "K": 11008, "na": 86, "dense": False, "select": True, "plan": [4, 16, 8, 4, 64, 4],
+         "us": 1.0},
+        {"bt": 16, "N": 4096, "K": 11008, "na": 86, "dense": False, "plan": [2, 32, 2, 4, 16, 1], "us": 1.0},
+        {"bt": 64, "N": 4096, "K": 11008, "na": 172, "dense": True, "plan": [8, 16, 8, 4, 64, 2], "us": 1.0},
+    ]}))
+    tuning.load_table(str(path))
+    try:
+        assert tuning.lookup(64, 4096, 172, 83).as_tuple() == (4, 16, 4, 4, 64, 2)
+        assert tuning.lookup(64, 4096, 172, 83, select=True).as_tuple() == (4, 16, 8, 4, 64, 4)
+        assert tuning.lookup(16, 4096, 172, 83, select=True).as_tuple() == (2, 32, 2, 4, 16, 1)
+        assert tuning.lookup(64, 4096, 172, 172, dense=True, select=True).as_tuple() == (8, 16, 8, 4, 64, 2)
+    finally:
+        tuning.load_table()
 
 
 def test_lookup_row_groups_only_as_tuned(tmp_path):

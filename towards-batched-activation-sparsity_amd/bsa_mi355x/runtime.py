@@ -199,16 +199,16 @@ def make_plan(num_split_k: Optional[int] = None, tile_b: Optional[int] = None, t
 
 
 def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan: Optional[Plan] = None,
-                 dense: bool = False, lookup_plan: bool = True) -> Plan:
+                 dense: bool = False, lookup_plan: bool = True, select: bool = False) -> Plan:
     """Resolve a (partial) plan for a problem.  With no plan (or an all-zero one) the tuned
-    table (tuning.lookup) is consulted first; remaining zero fields are filled by the library's
-    heuristics; tile fields that name a kernel that is not instantiated fall back to automatic
-    (the split-K factor is kept)."""
+    table (tuning.lookup; select=True: the entries timed as selection + GEMM first) is consulted
+    first; remaining zero fields are filled by the library's heuristics; tile fields that name a
+    kernel that is not instantiated fall back to automatic (the split-K factor is kept)."""
     lib = load()
     if lookup_plan and (plan is None or not any(plan.as_tuple())):
         from . import tuning
 
-        tuned = tuning.lookup(bt, n, nblk, na, dense=dense)
+        tuned = tuning.lookup(bt, n, nblk, na, dense=dense, select=select)
         if tuned is not None:
             plan = tuned
     req = Plan(*(plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0, 0)))

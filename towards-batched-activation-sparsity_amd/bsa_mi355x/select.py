@@ -220,7 +220,7 @@ def select_gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: i
         idx_out = torch.empty(max(kk, 1), dtype=torch.int32, device=dev)
     if count_out is None:
         count_out = torch.empty(1, dtype=torch.int32, device=dev)
-    pl = resolve_plan(bt, n_dim, nblk, kk, dev, plan)
+    pl = resolve_plan(bt, n_dim, nblk, kk, dev, plan, select=True)
     sel_bytes = int(lib.bsg_select_workspace_bytes(m_dim))
     gemm_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
     ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes, (bt, n_dim) + pl.as_tuple())

@@ -61,10 +61,12 @@ def load_table(path: str = TABLE_PATH) -> List[dict]:
     return entries
 
 
-def lookup(bt: int, n: int, nblk: int, na: int, dense: bool = False) -> Optional[Plan]:
+def lookup(bt: int, n: int, nblk: int, na: int, dense: bool = False, select: bool = False) -> Optional[Plan]:
     """Best tabulated plan for (bt, N, nblk, na): same N and block count, same 16/32/64-row
     bucket, nearest batch, then the dense entry (dense=True) or the nearest active-block count.
-    None when the shape is not tabulated."""
+    select=True (a selection + GEMM, whose GEMM ranks the block scores itself) prefers the
+    entries timed that way (refine_select) and falls back to the plain GEMM's.  None when the
+    shape is not tabulated."""
     if _TABLE is None:
         load_table()
     cands = _INDEX.get((int(n), int(nblk)))
@@ -72,6 +74,14 @@ def lookup(bt: int, n: int, nblk: int, na: int, dense: bool = False) -> Optional
         return None
     rb = rows_bucket(bt)
     same = [e for e in cands if rows_bucket(int(e["bt"])) == rb]
+    if select and not dense:
+        sel = [e for e in same if e.get("select")]
+        if sel:
+            same = sel
+        else:
+            same = [e for e in same if not e.get("select")]
+    else:
+        same = [e for e in same if not e.get("select")]
     if not same:
         return None
     best_bt = min({int(e["bt"]) for e in same}, key=lambda b: (abs(b - bt), b))
@@ -202,20 +212,29 @@ class _Case:
         self.idx = perm.sort()[0].to(torch.int32).to(device)
         self.y = torch.empty(bt, n, dtype=torch.float16, device=device)
 
-    def time(self, plan: Optional[Plan], dense: bool = False, reps: int = 5) -> float:
+    def time(self, plan: Optional[Plan], dense: bool = False, reps: int = 5, select: bool = False) -> float:
         """Median µs per launch over `reps` graph replays of R rotated launches, R copies holding
-        >= rotate_bytes of the blocks this launch reads (so the Infinity Cache serves no repeat)."""
+        >= rotate_bytes of the blocks this launch reads (so the Infinity Cache serves no repeat).
+        select=True times the exact-L1 selection (k = the case's block count) + GEMM instead."""
         import torch
 
         from .runtime import gemm_packed
+        from .select import select_gemm_packed
 
         na = self.nblk if dense else int(self.idx.numel())
         use = self.packed[: min(len(self.packed), _rotation(na * BLOCK_K * self.n * 2, self.rotate_bytes))]
+        if select:
+            sel_idx = torch.empty(max(na, 1), dtype=torch.int32, device=self.x.device)
+            sel_cnt = torch.empty(1, dtype=torch.int32, device=self.x.device)
 
         def run():
             for p in use:
-                gemm_packed(self.x, p, self.n, None if dense else self.idx, self.y, plan=plan,
-                            workspace_prefix="tune")
+                if select:
+                    select_gemm_packed(self.x, p, self.n, na, self.y, plan=plan, idx_out=sel_idx, count_out=sel_cnt,
+                                       workspace_prefix="tune_sel")
+                else:
+                    gemm_packed(self.x, p, self.n, None if dense else self.idx, self.y, plan=plan,
+                                workspace_prefix="tune")
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -241,23 +260,23 @@ class _Case:
         return statistics.median(ts)
 
 
-def _time_or_inf(case: "_Case", plan: Plan, dense: bool = False) -> float:
+def _time_or_inf(case: "_Case", plan: Plan, dense: bool = False, select: bool = False) -> float:
     """A candidate the library rejects for this case (BsgUnsupported) never wins."""
     from ._lib import BsgUnsupported
 
     try:
-        return case.time(plan, dense=dense)
+        return case.time(plan, dense=dense, select=select)
     except BsgUnsupported:
         return float("inf")
 
 
 def _pick(case: "_Case", plans: Sequence[Plan], dense: bool = False, margin: float = 0.05, finalists: int = 4,
-          rounds: int = 3) -> Tuple[float, Optional[Plan]]:
+          rounds: int = 3, select: bool = False) -> Tuple[float, Optional[Plan]]:
     """Best plan for a case: every candidate is timed once; those within `margin` of the best
     (at most `finalists`) are timed `rounds` more times, interleaved, and the lowest median wins
     (one timing each lets plans a few percent apart swap places from run to run)."""
-    first = sorted(((us, p) for p in plans for us in [_time_or_inf(case, p, dense=dense)] if math.isfinite(us)),
-                   key=lambda t: t[0])
+    first = sorted(((us, p) for p in plans for us in [_time_or_inf(case, p, dense=dense, select=select)]
+                    if math.isfinite(us)), key=lambda t: t[0])
     if not first:
         return float("inf"), None
     fin = [t for t in first if t[0] <= first[0][0] * (1.0 + margin)][:finalists]
@@ -266,7 +285,7 @@ def _pick(case: "_Case", plans: Sequence[Plan], dense: bool = False, margin: flo
     samples = [[us] for us, _ in fin]
     for _ in range(rounds):
         for i, (_, p) in enumerate(fin):
-            samples[i].append(case.time(p, dense=dense))
+            samples[i].append(case.time(p, dense=dense, select=select))
     i = min(range(len(fin)), key=lambda j: statistics.median(samples[j]))
     return statistics.median(samples[i]), fin[i][1]
 
@@ -344,7 +363,7 @@ def refine(shapes: Sequence[str], batch_sizes: Sequence[int], kinds: Sequence[in
         k, n = LLAMA2_7B_SHAPES[sname]
         nblk = (k + BLOCK_K - 1) // BLOCK_K
         for bt in batch_sizes:
-            rows = [e for e in entries if e["shape"] == sname and int(e["bt"]) == bt]
+            rows = [e for e in entries if e["shape"] == sname and int(e["bt"]) == bt and not e.get("select")]
             if not rows:
                 continue
             min_na = min(int(e["na"]) for e in rows)
@@ -375,6 +394,61 @@ def refine(shapes: Sequence[str], batch_sizes: Sequence[int], kinds: Sequence[in
     return entries
 
 
+def refine_select(shapes: Sequence[str], batch_sizes: Sequence[int], table: str = TABLE_PATH,
+                  out_table: Optional[str] = None, rotate_bytes: int = 1 << 30, seed: int = 1234,
+                  shortlist: int = 12, log=print) -> List[dict]:
+    """Add or re-time the selection + GEMM entries ("select": true) of the table: for every sparse
+    entry of the given shapes and batches, the exact-L1 selection of that many blocks followed by
+    the GEMM that ranks the scores itself (select.select_gemm_packed, rotated like the GEMM's
+    entries) is timed with the `shortlist` plans that are fastest as a plain GEMM and the plain
+    GEMM's tabulated plan, and the fastest is kept.  The in-GEMM rank costs a work-group a cold load of the scores plus nblk^2
+    compares spread over its waves, so the best plan can differ from the plain GEMM's."""
+    import torch
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    with open(table) as f:
+        data = json.load(f)
+    entries = data["entries"]
+    t_start = time.time()
+    for sname in shapes:
+        k, n = LLAMA2_7B_SHAPES[sname]
+        nblk = (k + BLOCK_K - 1) // BLOCK_K
+        for bt in batch_sizes:
+            rows = [e for e in entries if e["shape"] == sname and int(e["bt"]) == bt and not e["dense"]
+                    and not e.get("select")]
+            if not rows:
+                continue
+            min_na = min(int(e["na"]) for e in rows)
+            case = _Case(bt, k, n, nblk, seed, dev, rotate_bytes, min_na=min_na)
+            gen = torch.Generator().manual_seed(seed)
+            for e in sorted(rows, key=lambda e: int(e["na"])):
+                na = int(e["na"])
+                case.idx = torch.randperm(nblk, generator=gen)[:na].sort()[0].to(torch.int32).to(dev)
+                base = Plan(*e["plan"])
+                # every candidate timed as a plain GEMM first; the `shortlist` fastest (and the plain
+                # GEMM's tabulated plan) are then timed as selection + GEMM
+                plain = sorted(((us, p) for p in candidate_plans(bt, na, nblk) for us in [_time_or_inf(case, p)]
+                                if math.isfinite(us)), key=lambda t: t[0])
+                cands = [base] + [p for _, p in plain[:shortlist] if p.as_tuple() != base.as_tuple()]
+                best_us, best = _pick(case, cands, select=True)
+                base_us = statistics.median([case.time(base, select=True) for _ in range(3)])
+                old = [x for x in entries if x.get("select") and x["shape"] == sname and int(x["bt"]) == bt
+                       and int(x["na"]) == na]
+                for x in old:
+                    entries.remove(x)
+                plan = best if best is not None else base
+                entries.append({"shape": sname, "bt": bt, "N": n, "K": k, "na": na, "dense": False, "select": True,
+                                "plan": list(plan.as_tuple()), "us": round(best_us if best else base_us, 3)})
+                log(f"[select {time.time() - t_start:6.1f}s] {sname} B={bt} na={na}: {plan.as_tuple()} "
+                    f"{best_us:.2f} us (plain GEMM's plan {base.as_tuple()}: {base_us:.2f} us)")
+            del case
+            torch.cuda.empty_cache()
+    with open(out_table or table, "w") as f:
+        json.dump(data, f, indent=1)
+    load_table(out_table or table)
+    return entries
+
+
 def main(argv: Optional[Iterable[str]] = None) -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shapes", default="qkvo,gate_up,down")
@@ -386,8 +460,14 @@ def main(argv: Optional[Iterable[str]] = None) -> None:
                     help="keep the other (shape, batch) entries of the shipped table in the output")
     ap.add_argument("--refine-kinds", default=None,
                     help="instead of a full search, re-time the shipped entries against these kinds (e.g. 5,6)")
-    ap.add_argument("--table", default=TABLE_PATH, help="--refine-kinds: the table to start from")
+    ap.add_argument("--table", default=TABLE_PATH, help="--refine-kinds / --select: the table to start from")
+    ap.add_argument("--select", action="store_true",
+                    help="add the selection + GEMM entries (refine_select) for --shapes x --batch-sizes")
     args = ap.parse_args(list(argv) if argv is not None else None)
+    if args.select:
+        refine_select(args.shapes.split(","), [int(b) for b in args.batch_sizes.split(",")], table=args.table,
+                      out_table=args.out, log=lambda m: print(m, flush=True))
+        return
     if args.refine_kinds:
         refine(args.shapes.split(","), [int(b) for b in args.batch_sizes.split(",")],
                kinds=[int(v) for v in args.refine_kinds.split(",")], table=args.table, out_table=args.out,
