@@ -14,9 +14,11 @@ bytes), so every replay streams at least 1 GiB of distinct active weight and the
 Cache cannot serve a repeat.  A "step" is one replay of a graph holding every point's R launches.
 
 value        = active-weight bytes of all GEMMs in the timed steps / timed seconds (GB/s)
-roofline     = the gate/up B=64 s=0.52 GEMM, the largest sparse point: algorithmic bytes
-               na*64*N*2 per launch over the average launch duration, from HIP events on the
-               launch stream around that point's graph replays
+roofline     = the dominant kernel (largest share of a step's GPU time, `by_kernel`) at its
+               largest sparse launch (gate/up B=64 s=0.52 with the shipped plans): algorithmic
+               bytes na*64*N*2 per launch over the average launch duration, from HIP events on the
+               launch stream around that point's graph replays; the CPU-reference configuration
+               (down_proj B=16 s=0.5) rides along as roofline.cpu_reference_point
 cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host core) on the
                configs[0] point, down_proj B=16 with 86 of 172 blocks; every point also carries
                its own CPU time
@@ -61,6 +63,7 @@ TRAFFIC_PROFILES = {
 }
 # MFMA utilisation from counters (SQ_VALU_MFMA_BUSY_CYCLES) of the roofline point's kernel.
 MFMA_PROFILES = {
+    "down_b16_s500": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_down_b16_s500.md"),
     "gate_up_b64_s520": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_gate_up_b64_s520.md"),
 }
 # Kernel (symbol prefix) that each plan kind launches.
@@ -555,29 +558,39 @@ def run_matrix(args, dev):
         out_points.append(row)
         log(json.dumps(row))
 
-    focus = "gate_up_b64_s520" if args.workload == "llama" else "down_b16_s500"
-    if args.only:
-        focus = points[0].name
-    fp = next(p for p in points if p.name == focus)
-    f_med, f_mean = per[focus]
-    achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(focus),
-                "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": focus,
-                "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes,
-                "plan": list(fp.plan.as_tuple())}
-    mf = load_mfma_util(focus)
-    if mf is not None:
-        roofline["mfma_util_counter"] = mf
-    roofline["by_kernel"] = kernel_shares(points, per)
+    shares = kernel_shares(points, per)
+    focus = roofline_point(points, shares) if not args.only else points[0].name
+
+    def roofline_of(name, with_read):
+        fp = next(p for p in points if p.name == name)
+        f_med, f_mean = per[name]
+        achieved = fp.active_bytes / (f_mean * 1e-6) / 1e9
+        r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(name),
+             "kernel": KERNEL_NAMES.get(fp.plan.kind, "bsg_gemm"), "point": name,
+             "avg_launch_us": round(f_mean, 3), "bytes_per_launch": fp.active_bytes,
+             "plan": list(fp.plan.as_tuple())}
+        mf = load_mfma_util(name)
+        if mf is not None:
+            r["mfma_util_counter"] = mf
+        if with_read:
+            rd = read_calibration_us(fp)
+            r["practical_read"] = {
+                "us_per_launch": round(rd, 3), "GBps": round(fp.active_bytes / (rd * 1e-6) / 1e9, 1),
+                "frac_of_it": round(rd / f_mean, 4),
+                "what": "bsg_read_calibrate streaming the same bytes per launch (weight-load pattern, no compute), "
+                        "same rotation and timing"}
+            log(f"practical read of {fp.active_bytes / 1e6:.2f} MB: {rd:.2f} us ({r['practical_read']['GBps']} GB/s)")
+        return r
+
+    roofline = roofline_of(focus, not args.only)
+    roofline["chosen_as"] = ("the dominant kernel (largest share of the step's GPU time, by_kernel) at its "
+                             "largest sparse launch" if not args.only else "the --only point")
+    roofline["by_kernel"] = shares
+    if not args.only and focus != "down_b16_s500" and any(p.name == "down_b16_s500" for p in points):
+        # the CPU-reference configuration beside it
+        roofline["cpu_reference_point"] = roofline_of("down_b16_s500", True)
     if not args.only:
-        rd = read_calibration_us(fp)
-        roofline["practical_read"] = {
-            "us_per_launch": round(rd, 3), "GBps": round(fp.active_bytes / (rd * 1e-6) / 1e9, 1),
-            "frac_of_it": round(rd / f_mean, 4),
-            "what": "bsg_read_calibrate streaming the same bytes per launch (weight-load pattern, no compute), "
-                    "same rotation and timing"}
-        log(f"practical read of {fp.active_bytes / 1e6:.2f} MB: {rd:.2f} us ({roofline['practical_read']['GBps']} GB/s)")
         for p, row in zip(points, out_points):
             if p.dense and p.bt == 16:
                 row["torch_mm_us"] = round(torch_mm_us(p), 3)
@@ -617,7 +630,7 @@ def run_matrix(args, dev):
     cpu = None
     if not args.no_cpu and not args.only:
         log("cpu baseline ...")
-        cpu_pt = next((p for p in points if p.name == "down_b16_s500"), fp)
+        cpu_pt = next((p for p in points if p.name == "down_b16_s500"), next(p for p in points if p.name == focus))
         cpu = cpu_baseline(cpu_pt, args.cpu_seconds)
         for p, row in zip(points, out_points):
             row["cpu_us_per_gemm"] = round(cpu_point_us(p), 1)
@@ -660,6 +673,17 @@ def run_matrix(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def roofline_point(points, shares):
+    """The roofline point: the dominant kernel (largest share of the step's GPU time) at its
+    largest sparse launch (most active-weight bytes per launch, a streaming launch rather than a
+    latency-bound one); the dominant kernel's largest launch of any kind when it runs no sparse
+    point."""
+    dominant = next(iter(shares))  # kernel_shares orders by time share
+    mine = [p for p in points if KERNEL_NAMES.get(p.plan.kind, "bsg_gemm") == dominant]
+    sparse = [p for p in mine if not getattr(p, "dense", False)] or mine
+    return max(sparse, key=lambda p: (p.active_bytes, p.name)).name
+
+
 def kernel_shares(points, per):
     """Per kernel (symbol prefix of the plans' kinds): its share of one step's GPU time (each point
     weighted by its launches per step), and active-weight bytes over that time against the peak."""
@@ -667,16 +691,18 @@ def kernel_shares(points, per):
     for p in points:
         name = KERNEL_NAMES.get(p.plan.kind, "bsg_gemm")
         us = per[p.name][1] * p.copies
-        a = acc.setdefault(name, {"us": 0.0, "bytes": 0, "points": []})
+        a = acc.setdefault(name, {"us": 0.0, "bytes": 0, "points": [], "top": (0.0, None)})
         a["us"] += us
         a["bytes"] += p.active_bytes * p.copies
         a["points"].append(p.name)
+        if us > a["top"][0]:
+            a["top"] = (us, p.name)
     total = sum(a["us"] for a in acc.values())
     out = {}
     for name, a in sorted(acc.items(), key=lambda kv: -kv[1]["us"]):
         gbs = a["bytes"] / (a["us"] * 1e-6) / 1e9
         out[name] = {"time_share": round(a["us"] / total, 4), "GBps": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "points": a["points"]}
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "points": a["points"], "top_point": a["top"][1]}
     return out
 
 

@@ -201,22 +201,48 @@ def test_bench_traffic_profile_per_roofline_point():
 
 
 def test_bench_roofline_profiles_match_the_tuned_kernel():
-    """The committed traffic and counter summaries of the llama roofline point were taken on the
-    kernel its tuned plan launches now (a retune that changes the kernel makes them stale)."""
+    """The committed traffic and counter summaries of the llama roofline points (the dominant
+    kernel's CPU-reference point, down B=16 s=0.5, and the largest sparse point, gate/up B=64
+    s=0.52) were taken on the kernel their tuned plans launch now (a retune that changes the kernel
+    makes them stale)."""
     bench = _bench_module()
     from bsa_mi355x import tuning
 
-    plan = tuning.lookup(64, 11008, 64, 31)
-    assert plan is not None
-    kern = bench.KERNEL_NAMES[plan.kind]
-    for prof in (bench.TRAFFIC_PROFILES["gate_up_b64_s520"], bench.MFMA_PROFILES["gate_up_b64_s520"]):
-        with open(prof) as f:
-            text = f.read()
-        assert kern in text, (prof, kern)
-        assert ",".join(str(v) for v in plan.as_tuple()) in text.replace(" ", ""), (prof, plan)
-    mf = bench.load_mfma_util("gate_up_b64_s520")
-    assert mf is not None and 0.0 < mf["value"] < 1.0
+    for point, (bt, n, nblk, na) in (("gate_up_b64_s520", (64, 11008, 64, 31)),
+                                     ("down_b16_s500", (16, 4096, 172, 86))):
+        plan = tuning.lookup(bt, n, nblk, na)
+        assert plan is not None
+        kern = bench.KERNEL_NAMES[plan.kind]
+        for prof in (bench.TRAFFIC_PROFILES[point], bench.MFMA_PROFILES[point]):
+            with open(prof) as f:
+                text = f.read()
+            assert kern in text, (prof, kern)
+            assert ",".join(str(v) for v in plan.as_tuple()) in text.replace(" ", ""), (prof, plan)
+        mf = bench.load_mfma_util(point)
+        assert mf is not None and 0.0 < mf["value"] < 1.0
     assert bench.load_mfma_util("qkvo_b2_s803") is None
+
+
+class _P:
+    def __init__(self, name, kind, copies, active, dense=False):
+        self.name, self.copies, self.active_bytes, self.dense = name, copies, active, dense
+        self.plan = bsa.Plan(1, 16, 2, 4, 16, kind)
+
+
+def test_bench_roofline_point_is_the_dominant_kernels_largest_sparse_launch():
+    """The roofline goes on the kernel with the largest share of the step's GPU time, at its
+    sparse point with the most active-weight bytes per launch."""
+    bench = _bench_module()
+    pts = [_P("down_b16_s500", 1, 10, 45), _P("down_b16_dense", 1, 5, 90, dense=True),
+           _P("qkvo_b2_s803", 6, 100, 7), _P("gate_up_b64_s520", 6, 20, 44)]
+    per = {"down_b16_s500": (11.0, 11.0), "down_b16_dense": (17.0, 17.0), "qkvo_b2_s803": (3.6, 3.6),
+           "gate_up_b64_s520": (13.7, 13.7)}
+    shares = bench.kernel_shares(pts, per)
+    assert next(iter(shares)) == "bsg_gemm_vt_kernel" and shares["bsg_gemm_vt_kernel"]["top_point"] == "qkvo_b2_s803"
+    assert bench.roofline_point(pts, shares) == "gate_up_b64_s520"
+    per["down_b16_s500"] = (80.0, 80.0)  # kind 1 now dominates the step
+    shares = bench.kernel_shares(pts, per)
+    assert bench.roofline_point(pts, shares) == "down_b16_s500"  # its largest sparse launch, not the dense one
 
 
 def _bench_module():
