@@ -122,6 +122,18 @@ int bsg_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K,
              void* y, int64_t ldy, int dtype,
              void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
+/* bsg_gemm with the list sorted ascending inside the GEMM's own list staging (no separate sort
+ * launch): the same arguments, the same result as an ascending sort of the list followed by
+ * bsg_gemm, bit for bit.  num_active <= BSG_MAX_NBLK / 2 (else BSG_ERR_UNSUPPORTED).
+ * Replaces the sort + GEMM pair of _prepacked_block_sparse_gemm_from_active_blocks with
+ * sort_active_blocks=True: _sort_active_blocks_asc (…min_runtime.py:140-163, called at
+ * :3193-3194) followed by prepacked_block_sparse_gemm_batched_kernel (…min_runtime.py:684-733). */
+int bsg_gemm_sorted(const void* x, int64_t ldx, int64_t bt, int64_t K,
+                    const void* wp, int64_t N,
+                    const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev,
+                    void* y, int64_t ldy, int dtype,
+                    void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
 /* Same GEMM driven by a u8 bitmap[total_k_blocks] (non-zero = active; 1 <= total_k_blocks <=
  * ceil(K/64), later blocks count as inactive), compacted on the
  * device into ascending block order; the block list never leaves the GPU.

@@ -134,6 +134,17 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert call(K=200000) == _lib.BSG_ERR_UNSUPPORTED
     assert "workspace" in _lib.last_error() or "K" in _lib.last_error()
 
+    def call_sorted(**kw):
+        a = dict(ok, **kw)
+        return lib.bsg_gemm_sorted(a["x"], a["ldx"], a["bt"], a["K"], a["wp"], a["N"], a["idx"], a["na"], a["nad"],
+                                   a["y"], a["ldy"], a["dtype"], a["ws"], a["ws_bytes"], ctypes.byref(p), None)
+
+    # the in-kernel sort takes at most BSG_MAX_NBLK / 2 entries
+    assert call_sorted(na=_lib.MAX_NBLK // 2 + 1, K=64 * _lib.MAX_NBLK, ldx=64 * _lib.MAX_NBLK) == _lib.BSG_ERR_UNSUPPORTED
+    assert "sort" in _lib.last_error()
+    assert call_sorted(na=-1) == _lib.BSG_ERR_ARG
+    assert call_sorted(idx=None) == _lib.BSG_ERR_ARG
+
 
 def test_2d_entry_points_reject_bad_arguments_without_launching():
     lib = bsa.load()

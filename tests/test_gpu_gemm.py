@@ -351,6 +351,74 @@ def test_maximum_block_count(dev):
     assert np.array_equal(idx.cpu().numpy()[:1000], orc.select_topk_l1(x, 1000))
 
 
+SORT_LISTS = {
+    "random": np.random.default_rng(21).permutation(64)[:29],
+    "descending": np.arange(63, 5, -2),
+    "ascending": np.arange(3, 64, 3),
+    "duplicates": np.array([5, 3, 5, 60, 0, 3, 3]),
+    "out_of_range": np.array([7, -3, 64, 2, 1000, 7, -2147483648, 2147483647]),
+    "single": np.array([42]),
+}
+
+
+@pytest.mark.parametrize("plan", [(1, 16, 2, 4, 16, 1), (3, 16, 4, 4, 32, 2), (2, 16, 8, 4, 64, 4), (1, 16, 4, 4, 4, 3),
+                                  (1, 48, 4, 4, 16, 5), (1, 16, 4, 4, 16, 6)])
+def test_in_kernel_sort_matches_sort_then_gemm(dev, plan):
+    """bsg_gemm_sorted (the list sorted in the GEMM's own staging) gives, bit for bit, what an
+    ascending sort of the list followed by bsg_gemm gives (KRN:3193-3194 then KRN:684-733), for
+    unsorted, descending, already ascending, duplicated and out-of-range lists, on every kernel
+    kind; a device count sorts only the first entries it names."""
+    bt, k, n = 8, 4096, 1000
+    x, w_nk, _ = case(22, bt, k, n, 1)
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    p = bsa.Plan(*plan)
+    for name, ids in SORT_LISTS.items():
+        ids = ids.astype(np.int32)
+        print(f"in-kernel sort plan={plan} list={name} na={ids.size}", flush=True)
+        got = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        want = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        bsa.gemm_packed(xt, packed, n, to_dev(ids, dev), got, plan=p, workspace_prefix="isort", sort_list=True)
+        bsa.gemm_packed(xt, packed, n, to_dev(np.sort(ids), dev), want, plan=p, workspace_prefix="isort_ref")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{name}: in-kernel sort differs from sort + GEMM"
+        valid = ids[(ids >= 0) & (ids < 64)]
+        assert_close(got.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.sort(valid)), f"sorted {name}")
+    ids = SORT_LISTS["random"].astype(np.int32)[:20]
+    got = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+    bsa.gemm_packed(xt, packed, n, to_dev(ids, dev), got, num_active=20,
+                    num_active_dev=to_dev(np.array([12], dtype=np.int32), dev), plan=p, workspace_prefix="isort",
+                    sort_list=True)
+    torch.cuda.synchronize()
+    assert_close(got.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.sort(ids[:12])), "device count")
+
+
+def test_in_kernel_sort_at_its_limit_and_past_it(dev):
+    """1024 entries (MAX_NBLK // 2, the in-kernel sort's limit) sorted in the GEMM; the drop-in
+    sorts a longer list with a sort launch first (same result)."""
+    bt, k, n = 3, 64 * 2048, 48
+    x, w_nk, _ = case(23, bt, k, n, 1)
+    xt = to_dev(x, dev)
+    wt = to_dev(w_nk, dev)
+    packed = bsa.pack_weight(wt)
+    perm = np.random.default_rng(6).permutation(2048).astype(np.int32)
+    got = torch.empty(bt, n, dtype=F16, device=dev)
+    want = torch.empty(bt, n, dtype=F16, device=dev)
+    bsa.gemm_packed(xt, packed, n, to_dev(perm[:1024], dev), got, workspace_prefix="isort_max", sort_list=True)
+    bsa.gemm_packed(xt, packed, n, to_dev(np.sort(perm[:1024]), dev), want, workspace_prefix="isort_max_ref")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert_close(got.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.sort(perm[:1024])), "1024 sorted in-kernel")
+    with pytest.raises(ValueError):
+        bsa.gemm_packed(xt, packed, n, to_dev(perm[:1025], dev), got, workspace_prefix="isort_max", sort_list=True)
+    out = torch.empty(bt, 1, n, dtype=F16, device=dev)
+    bsa._prepacked_block_sparse_gemm_from_active_blocks(xt.view(bt, 1, k), wt, to_dev(perm[:1500], dev), out,
+                                                        cache_prefix="isort_long")
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.sort(perm[:1500])),
+                 "1500 sorted by a sort launch")
+
+
 @pytest.mark.parametrize("plan", [(1, 16, 2, 4, 16, 1), (3, 16, 4, 4, 32, 2), (2, 16, 8, 4, 64, 4), (1, 16, 4, 4, 4, 3)])
 def test_strided_rows_and_side_stream(dev, plan):
     """X and Y as row-strided views (ldx > K, ldy > N), launched on a side stream: the padding

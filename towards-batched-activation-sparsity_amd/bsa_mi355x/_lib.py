@@ -114,6 +114,8 @@ SIGNATURES = {
     "bsg_gemm_workspace_bytes": (_i64, [_i64, _i64, _pplan]),
     "bsg_workspace_init": (_int, [_vp, _i64, _vp]),
     "bsg_gemm": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
+    "bsg_gemm_sorted": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _int, _vp, _i64, _pplan,
+                               _vp]),
     "bsg_gemm_bitmap": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_gemm_dense": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_gemm_2d": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i32, _vp, _int, _vp, _i64, _int,

@@ -198,6 +198,11 @@ def make_plan(num_split_k: Optional[int] = None, tile_b: Optional[int] = None, t
     return p
 
 
+# The library's plan resolution is a pure function of (problem, CU count, requested plan); its
+# answers are kept so that an eager call pays one dictionary lookup instead of a library call.
+_RESOLVED: dict = {}
+
+
 def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan: Optional[Plan] = None,
                  dense: bool = False, lookup_plan: bool = True, select: bool = False) -> Plan:
     """Resolve a (partial) plan for a problem.  With no plan (or an all-zero one) the tuned
@@ -211,13 +216,18 @@ def resolve_plan(bt: int, n: int, nblk: int, na: int, device: torch.device, plan
         tuned = tuning.lookup(bt, n, nblk, na, dense=dense, select=select)
         if tuned is not None:
             plan = tuned
-    req = Plan(*(plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0, 0)))
-    out = Plan(*req.as_tuple())
-    rc = lib.bsg_plan_resolve(bt, n, nblk, na, _cu_count(device), ctypes_byref(out))
+    req = plan.as_tuple() if plan is not None else (0, 0, 0, 0, 0, 0)
+    key = (int(bt), int(n), int(nblk), int(na), _cu_count(device), req)
+    hit = _RESOLVED.get(key)
+    if hit is not None:
+        return Plan(*hit)
+    out = Plan(*req)
+    rc = lib.bsg_plan_resolve(bt, n, nblk, na, key[4], ctypes_byref(out))
     if rc == _lib.BSG_ERR_UNSUPPORTED:
-        out = Plan(req.split_k, 0, 0, 0, 0, 0)
-        rc = lib.bsg_plan_resolve(bt, n, nblk, na, _cu_count(device), ctypes_byref(out))
+        out = Plan(req[0], 0, 0, 0, 0, 0)
+        rc = lib.bsg_plan_resolve(bt, n, nblk, na, key[4], ctypes_byref(out))
     check(rc)
+    _RESOLVED[key] = out.as_tuple()
     return out
 
 
@@ -328,11 +338,13 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
                 y2d: torch.Tensor, *, num_active: Optional[int] = None, num_active_dev: Optional[torch.Tensor] = None,
                 bitmap: Optional[torch.Tensor] = None, total_k_blocks: Optional[int] = None,
                 plan: Optional[Plan] = None, workspace_prefix: str = "gemm",
-                kernel: Optional[_KernelHandle] = None) -> Plan:
+                kernel: Optional[_KernelHandle] = None, sort_list: bool = False) -> Plan:
     """Launch one block-sparse GEMM on already packed weights (2-D x [bt, K], y [bt, N]).
 
     Exactly one source of active blocks: `active_blocks` (int32 device list, host length or
-    `num_active`; optional device count), `bitmap` (u8), or neither (dense: every block)."""
+    `num_active`; optional device count), `bitmap` (u8), or neither (dense: every block).
+    sort_list: the GEMM sorts the list ascending itself (bsg_gemm_sorted, at most
+    MAX_NBLK // 2 entries), with the result of an ascending sort followed by the GEMM."""
     lib = load()
     dev = _require_cuda(x2d, packed, y2d)
     code = _dtype_code(x2d)
@@ -353,8 +365,9 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
     elif active_blocks is not None:
         mode = "list"
         na = int(active_blocks.numel() if num_active is None else num_active)
-        if na > MAX_NBLK:
-            raise ValueError(f"{na} active blocks exceeds {MAX_NBLK}")
+        if na > (MAX_NBLK // 2 if sort_list else MAX_NBLK):
+            raise ValueError(f"{na} active blocks exceeds {MAX_NBLK // 2 if sort_list else MAX_NBLK}"
+                             + (" (in-kernel sort)" if sort_list else ""))
         na_for_plan = na
     else:
         mode = "dense"
@@ -375,7 +388,8 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
         with torch.cuda.device(dev):
             if mode == "list":
                 nad = num_active_dev.data_ptr() if num_active_dev is not None else None
-                return lib.bsg_gemm(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
+                entry = lib.bsg_gemm_sorted if sort_list else lib.bsg_gemm
+                return entry(x2d.data_ptr(), x2d.stride(0), bt, kd, packed.data_ptr(), n_dim,
                                     active_blocks.data_ptr() if na > 0 else None, na, nad, y2d.data_ptr(),
                                     y2d.stride(0), code, ws_ptr, ws_bytes, ctypes_byref(pl), stream)
             if mode == "bitmap":
@@ -483,12 +497,14 @@ def _prepacked_block_sparse_gemm_from_active_blocks(
     if ab.dtype != torch.int32:
         ab = ab.to(torch.int32)
     ab = ab.contiguous()
-    if int(ab.numel()) > num_blocks:
-        ab = ab[:num_blocks].contiguous()
-    if sort_active_blocks:
-        ab = _sort_active_blocks_asc(ab)
-    gemm_packed(x2d, entry.packed, n_dim, ab, y2d, plan=None, workspace_prefix=f"{cache_prefix}_ws",
-                kernel=prepacked_block_sparse_gemm_batched_kernel)
+    # the GEMM reads the first num_blocks entries; it sorts them itself (no sort launch) up to
+    # MAX_NBLK // 2 of them
+    in_kernel = sort_active_blocks and num_blocks <= MAX_NBLK // 2
+    if sort_active_blocks and not in_kernel:
+        ab = _sort_active_blocks_asc(ab[:num_blocks])
+    gemm_packed(x2d, entry.packed, n_dim, ab, y2d, num_active=num_blocks, plan=None,
+                workspace_prefix=f"{cache_prefix}_ws", kernel=prepacked_block_sparse_gemm_batched_kernel,
+                sort_list=in_kernel)
 
 
 def _prepacked_block_sparse_gemm_from_active_blocks_splitk(

@@ -35,6 +35,8 @@ LLAMA2_7B_SHAPES = {"qkvo": (4096, 4096), "gate_up": (4096, 11008), "down": (110
 
 _TABLE: Optional[List[dict]] = None
 _INDEX: Dict[Tuple[int, int], List[dict]] = {}
+# lookup() answers per (bt, N, nblk, na, dense, select), cleared whenever a table is loaded
+_MEMO: Dict[tuple, Optional[tuple]] = {}
 
 
 def rows_bucket(bt: int) -> int:
@@ -56,6 +58,7 @@ def load_table(path: str = TABLE_PATH) -> List[dict]:
     entries = [e for e in data.get("entries", []) if len(e.get("plan", ())) == 6]
     _TABLE = entries
     _INDEX = {}
+    _MEMO.clear()
     for e in entries:
         _INDEX.setdefault((int(e["N"]), (int(e["K"]) + BLOCK_K - 1) // BLOCK_K), []).append(e)
     return entries
@@ -69,7 +72,17 @@ def lookup(bt: int, n: int, nblk: int, na: int, dense: bool = False, select: boo
     shape is not tabulated."""
     if _TABLE is None:
         load_table()
-    cands = _INDEX.get((int(n), int(nblk)))
+    key = (int(bt), int(n), int(nblk), int(na), bool(dense), bool(select))
+    if key in _MEMO:
+        hit = _MEMO[key]
+        return None if hit is None else Plan(*hit)
+    p = _lookup(*key)
+    _MEMO[key] = None if p is None else p.as_tuple()
+    return p
+
+
+def _lookup(bt: int, n: int, nblk: int, na: int, dense: bool, select: bool) -> Optional[Plan]:
+    cands = _INDEX.get((n, nblk))
     if not cands:
         return None
     rb = rows_bucket(bt)

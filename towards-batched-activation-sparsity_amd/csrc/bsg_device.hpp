@@ -30,6 +30,8 @@ struct GemmParams {
   int32_t* idx_out;
   int32_t* na_out;
   int32_t keyed;
+  // MODE_LIST: sort the list ascending while staging it (at most BSG_MAX_NBLK / 2 entries)
+  int32_t sort_list;
   // 2-D sparsity: ascending active 64-column output blocks (null: every column), their count
   // (host value, or the device one when nn_dev is set), whether Y is compact (active blocks
   // side by side), and the width Y stores are bounded by (N, or nn * 64 when compact)
@@ -394,11 +396,48 @@ __device__ __forceinline__ bool tile_columns(const GemmParams& p, int tile, int 
   return true;
 }
 
+// The first na block ids in ascending order, into s_ids[0, na) (na <= BSG_MAX_NBLK / 2): the
+// sequence an ascending sort of the list gives (equal ids are equal, so their order does not
+// show).  The ids go to LDS as unsigned keys 0x7fffffff - id (descending in the id).  A list that
+// is already ascending is copied back; any other is ranked, each id's rank being the number of
+// entries before it in (id asc, list position asc) order, written to
+// s_ids[BSG_MAX_NBLK / 2 + rank] and copied back.  The rank loop reads the keys as LDS
+// broadcasts and keeps no array, so the kernels' register allocation is not disturbed.  Leaves
+// the copy-back unfenced; the caller's barrier follows.
+template <int NT>
+__device__ __forceinline__ void sort_block_list(const int32_t* ids, int na, int* s_ids) {
+  const int tid = threadIdx.x;
+  uint32_t* const s_key = (uint32_t*)s_ids;
+  for (int i = tid; i < na; i += NT) s_key[i] = (uint32_t)(0x7fffffffLL - (long long)ids[i]);
+  __syncthreads();
+  int unsorted = 0;
+  for (int i = tid; i + 1 < na; i += NT) unsorted |= s_key[i] < s_key[i + 1];
+  if (__syncthreads_or(unsorted)) {
+    int* const s_out = s_ids + BSG_MAX_NBLK / 2;
+    for (int i = tid; i < na; i += NT) {
+      const uint32_t ki = s_key[i];
+      int r = 0;
+#pragma unroll 8
+      for (int j = 0; j < na; ++j) {
+        const uint32_t kj = s_key[j];
+        r += (kj > ki) | ((kj == ki) & (j < i));
+      }
+      s_out[r] = (int)(0x7fffffffLL - (long long)ki);
+    }
+    __syncthreads();
+    for (int i = tid; i < na; i += NT) s_ids[i] = s_out[i];
+  } else {
+    // each thread rewrites only the entries it read
+    for (int i = tid; i < na; i += NT) s_ids[i] = (int)(0x7fffffffLL - (long long)s_key[i]);
+  }
+}
+
 // Stage this call's active-block list in LDS (list copy, bitmap compaction, top-k of block
 // scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
 // and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
-// second (up to 512 blocks).
-template <int NT>
+// second (up to 512 blocks).  SORT: the list may be sorted here (p.sort_list, a 1-D list launch
+// only; the 2-D forms are compiled without it).
+template <int NT, bool SORT>
 __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
   const int tid = threadIdx.x;
   int na;
@@ -413,7 +452,10 @@ __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids,
       const int d = *p.na_dev;
       na = d < 0 ? 0 : (d < na ? d : na);
     }
-    for (int i = tid; i < na; i += NT) s_ids[i] = p.idx[i];
+    if (SORT && p.sort_list)
+      sort_block_list<NT>(p.idx, __builtin_amdgcn_readfirstlane(na), s_ids);
+    else
+      for (int i = tid; i < na; i += NT) s_ids[i] = p.idx[i];
   } else if (p.mode == MODE_BITMAP) {
     const int per = (p.nbm + NT - 1) / NT;
     const int beg = tid * per < p.nbm ? tid * per : p.nbm;
@@ -567,7 +609,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // This wave's contiguous slice [pbeg, pend) of the list.
@@ -733,7 +775,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // The work-group's contiguous slice of the list (all its waves walk it together).
@@ -894,7 +936,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * w) / WPG);
   const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
@@ -1103,7 +1145,7 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, true>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * b) / WB);
   const int pend = (int)(((int64_t)na * (b + 1)) / WB);

@@ -705,6 +705,8 @@ struct LaunchExtras {
   float* part_fixed = nullptr;
   int64_t cnt_cap_tiles = 0;
   int64_t part_cap_bytes = 0;
+  // MODE_LIST: the kernel sorts the list ascending while staging it
+  int sort_list = 0;
 };
 
 int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp,
@@ -722,6 +724,8 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   if (mode == MODE_LIST) {
     if (na < 0 || na > BSG_MAX_NBLK) return fail(BSG_ERR_ARG, "num_active=%d (0..%d)", na, BSG_MAX_NBLK);
     if (na > 0 && !idx) return fail(BSG_ERR_ARG, "active_blocks is null");
+    if (ex.sort_list && na > BSG_MAX_NBLK / 2)
+      return fail(BSG_ERR_UNSUPPORTED, "in-kernel sort: num_active=%d (at most %d)", na, BSG_MAX_NBLK / 2);
   } else if (mode == MODE_TOPK) {
     if (!ex.scores || na < 0) return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)ex.scores, na);
     if (nblk > BSG_TOPK_MAX_NBLK)
@@ -803,6 +807,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.idx_out = ex.idx_out;
   p.na_out = ex.na_out;
   p.keyed = bt <= 64;
+  p.sort_list = mode == MODE_LIST && ex.sort_list && ex.nidx == nullptr;
   p.nidx = ex.nidx;
   p.nn_dev = ex.nn_dev;
   p.nn = ex.nn;
@@ -926,6 +931,15 @@ int bsg_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, 
              int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
   return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, active_blocks, num_active, num_active_dev, nullptr, 0, y,
                      ldy, dtype, ws, ws_bytes, plan, stream);
+}
+
+int bsg_gemm_sorted(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
+                    const int32_t* active_blocks, int32_t num_active, const int32_t* num_active_dev, void* y,
+                    int64_t ldy, int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  LaunchExtras ex;
+  ex.sort_list = 1;
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, active_blocks, num_active, num_active_dev, nullptr, 0, y,
+                     ldy, dtype, ws, ws_bytes, plan, stream, ex);
 }
 
 int bsg_gemm_bitmap(const void* x, int64_t ldx, int64_t bt, int64_t K, const void* wp, int64_t N,
