@@ -26,8 +26,9 @@ cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host
 The same line also carries, measured in the same run after the matrix (skip with --no-extras):
 fused_select_gemm = configs[3] (exact-L1 select k=31 of 64 + gate/up GEMM at B=64, indices
 checked bit-exact), decode_step = configs[4] (the 32-layer decode step of linears as one
-hipGraph), perstep_replay = the reference's headline table (its per-step sparsity maps of the
-224-GEMM decode step) at B=2, 4, 8, 16, 32, 64.
+hipGraph), eager_calls = the host cost of one eager call of the drop-in entry points (what
+the model patch pays per linear layer), perstep_replay = the reference's headline table (its
+per-step sparsity maps of the 224-GEMM decode step) at B=2, 4, 8, 16, 32, 64.
 
     python bench.py [--steps K] [--warmup W]
                     [--workload llama|down_sweep|fused|decode|perstep|2d] [--only POINT]
@@ -613,6 +614,8 @@ def run_matrix(args, dev):
         log("configs[4]: 32-layer decode step ...")
         extras["decode_step"] = measure_decode(args, dev)
         log(f"configs[4] done ({time.perf_counter() - t0:.1f} s): {extras['decode_step']['ms_per_step']} ms/step")
+        log("eager host cost of the drop-in entry points ...")
+        extras["eager_calls"] = measure_eager(args, dev)
         log("per-step replay of the reference's sparsity maps at every batch size ...")
         rows_ps, _, _ = measure_perstep(args, dev)
         extras["perstep_replay"] = {
@@ -780,6 +783,65 @@ def run_2d(args, dev):
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
+
+
+def measure_eager(args, dev):
+    """Host cost of one eager call of the drop-in entry points: no graph, what the reference's
+    model patch pays per linear layer (RRD:228-230 calls the runtime entry per forward).  At
+    down_proj B=16 s=0.5 with an unsorted list: host microseconds per call over back-to-back
+    calls, and wall microseconds per call once the GPU has drained (the larger of the host's
+    and the GPU's time per call).  The drop-in's output is checked against the oracle first."""
+    import numpy as np
+    import torch
+
+    import bsa_mi355x as bsa
+    from bsa_mi355x.select import select_gemm_packed
+    from oracle import bsg_oracle as orc
+
+    bt, (k, n), na, reps = 16, SHAPES["down"], 86, 2000
+    g = torch.Generator(device=dev)
+    g.manual_seed(SEED)
+    x = torch.randn(bt, 1, k, generator=g, device=dev).to(torch.float16)
+    w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.float16)
+    ids = torch.randperm(k // 64, generator=g, device=dev)[:na].to(torch.int32)  # unsorted
+    ids_sorted = torch.sort(ids)[0]
+    out = torch.empty(bt, 1, n, dtype=torch.float16, device=dev)
+    x2d, y2d = x.view(bt, k), out.view(bt, n)
+    packed = bsa.pack_weight(w)
+    wt = w.t().contiguous()
+    idx = torch.empty(na, dtype=torch.int32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    bsa._prepacked_block_sparse_gemm_from_active_blocks(x, w, ids, out, cache_prefix="eager_bench")
+    torch.cuda.synchronize()
+    y_ref = orc.gemm_ref(x2d.float().cpu().numpy(), w.float().cpu().numpy(), ids_sorted.cpu().numpy())
+    if not orc.within_tolerance(y2d.float().cpu().numpy(), y_ref):
+        raise SystemExit("eager drop-in output outside tolerance")
+    calls = {
+        "dropin_unsorted_list": lambda: bsa._prepacked_block_sparse_gemm_from_active_blocks(
+            x, w, ids, out, cache_prefix="eager_bench"),
+        "gemm_packed_table_plan": lambda: bsa.gemm_packed(x2d, packed, n, ids_sorted, y2d,
+                                                          workspace_prefix="eager_bench_packed"),
+        "select_gemm_packed": lambda: select_gemm_packed(x2d, packed, n, na, y2d, idx_out=idx, count_out=cnt,
+                                                         workspace_prefix="eager_bench_sel"),
+        "torch_mm_dense": lambda: torch.mm(x2d, wt, out=y2d),
+    }
+    res = {"workload": f"eager calls at down_proj B={bt} K={k} N={n}, {na}/{k // 64} blocks (s=0.5), "
+                       f"unsorted list for the drop-in; {reps} back-to-back calls per entry",
+           "what": "host_us = host time per call (Python + launch); wall_us = time per call until the GPU "
+                   "has drained (the larger of host and GPU time per call)"}
+    for name, fn in calls.items():
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        res[name] = {"host_us": round((t1 - t0) / reps * 1e6, 2), "wall_us": round((t2 - t0) / reps * 1e6, 2)}
+        log(f"eager {name}: host {res[name]['host_us']} us/call, wall {res[name]['wall_us']} us/call")
+    return res
 
 
 def measure_fused(args, dev):
