@@ -133,6 +133,99 @@ def test_fused_select_gemm_ties_and_repeats(dev):
     assert_close(y2, orc.gemm_ref(x2, w_nk, want2), "fused repeat")
 
 
+SELF_CASES = [  # (bt, K, N, k, plan): bt x K x 2 <= 24 KiB, so the GEMM scores the blocks itself
+    (1, 4096, 4096, 13, None), (2, 4096, 4096, 13, (1, 16, 4, 4, 16, 6)), (3, 4096, 11008, 31, (1, 16, 1, 4, 16, 1)),
+    (5, 1000, 300, 7, None), (8, 1024, 1000, 5, (1, 48, 4, 4, 16, 5)), (8, 1536, 4096, 11, (2, 16, 8, 4, 16, 4)),
+    (4, 3072, 4096, 20, (1, 16, 4, 4, 16, 6)), (1, 11008, 4096, 86, (2, 32, 4, 4, 16, 1)),
+    (7, 1536, 512, 0, None), (6, 2048, 512, 64, None),
+]
+
+
+@pytest.mark.parametrize("bt,kdim,n,k,plan", SELF_CASES)
+def test_self_scored_selection_in_one_launch(dev, bt, kdim, n, k, plan):
+    """At bt <= 8 and bt x K x 2 <= 24 KiB the selection + GEMM is one launch: every GEMM
+    work-group scores the blocks from x itself.  No score is written (the selector's part of the
+    workspace keeps a planted pattern); indices and count are bit-exact against the oracle; Y is
+    bit for bit the GEMM on the same list through bsg_gemm, and within tolerance of the oracle.
+    x holds ties (three equal blocks), a block far above the rest, a subnormal and -0."""
+    import ctypes
+
+    from bsa_mi355x import _lib
+    from bsa_mi355x.runtime import _stream_handle
+
+    x, w_nk, _ = case(900 + bt + k, bt, kdim, n, 1, "normal")
+    nb = -(-kdim // 64)
+    for j in (1, 4, nb - 1):
+        x[:, 64 * j:min(64 * j + 64, kdim)] = 7.0
+    x[0, 64 * 2:64 * 3] = np.float16(2048.0)
+    x[bt - 1, 64 * 3] = np.float16(2.0 ** -24)
+    x[bt // 2, 64 * 5] = -np.float16(0.0)
+    lib = bsa.load()
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    pl = bsa.resolve_plan(bt, n, nb, min(k, nb), dev, None if plan is None else bsa.Plan(*plan), select=True)
+    sel = int(lib.bsg_select_workspace_bytes(kdim))
+    gws = int(lib.bsg_gemm_workspace_bytes(bt, n, ctypes.byref(pl)))
+    ws = torch.zeros(sel + gws, dtype=torch.uint8, device=dev)
+    ws[256:sel] = 0xAB
+    y = torch.full((bt, n), float("nan"), dtype=torch.float16, device=dev)
+    idx = torch.full((max(k, 1),), -1, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    print(f"self-scored select+gemm bt={bt} K={kdim} N={n} k={k} plan={pl.as_tuple()}", flush=True)
+    rc = lib.bsg_select_gemm(xt.data_ptr(), kdim, bt, kdim, k, packed.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(),
+                             y.data_ptr(), n, 0, ws.data_ptr(), sel + gws, ctypes.byref(pl), _stream_handle(dev))
+    assert rc == _lib.BSG_OK, _lib.last_error()
+    torch.cuda.synchronize()
+    assert bool((ws[256:sel] == 0xAB).all()), "a score launch ran"
+    want = orc.select_topk_l1(x, k)
+    c = int(cnt.item())
+    assert c == len(want) == min(k, nb)
+    assert np.array_equal(idx.cpu().numpy()[:c], want)
+    y_list = torch.full((bt, n), float("nan"), dtype=torch.float16, device=dev)
+    bsa.gemm_packed(xt, packed, n, to_dev(want.astype(np.int32), dev) if c else None, y_list,
+                    num_active=c if c else None, plan=pl if c else None, workspace_prefix="t_self_ref")
+    torch.cuda.synchronize()
+    if c:
+        assert torch.equal(y, y_list), "one-launch selection + GEMM differs from the GEMM on its list"
+        assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), f"self-scored bt={bt} K={kdim}")
+    else:
+        assert torch.count_nonzero(y).item() == 0
+
+
+def test_two_launch_selection_above_the_self_scoring_size(dev):
+    """Above 24 KiB of activations (bt x K x 2) or 8 rows, and on the dot-product kernel (kind 3),
+    the score launch runs, writing the block scores into the selector's part of the workspace."""
+    import ctypes
+
+    from bsa_mi355x import _lib
+    from bsa_mi355x.runtime import _stream_handle
+
+    lib = bsa.load()
+    for bt, kdim, plan in ((16, 4096, (1, 16, 4, 4, 16, 1)), (4, 11008, (1, 16, 4, 4, 16, 1)),
+                           (4, 4096, (1, 16, 4, 4, 16, 6)), (2, 4096, (1, 16, 4, 4, 2, 3))):
+        n, k = 512, 20
+        x, w_nk, _ = case(950 + bt, bt, kdim, n, 1, "normal")
+        xt = to_dev(x, dev)
+        packed = bsa.pack_weight(to_dev(w_nk, dev))
+        pl = bsa.Plan(*plan)
+        sel = int(lib.bsg_select_workspace_bytes(kdim))
+        ws = torch.zeros(sel + int(lib.bsg_gemm_workspace_bytes(bt, n, ctypes.byref(pl))), dtype=torch.uint8,
+                         device=dev)
+        ws[256:sel] = 0xAB
+        y = torch.empty(bt, n, dtype=torch.float16, device=dev)
+        idx = torch.empty(k, dtype=torch.int32, device=dev)
+        cnt = torch.empty(1, dtype=torch.int32, device=dev)
+        rc = lib.bsg_select_gemm(xt.data_ptr(), kdim, bt, kdim, k, packed.data_ptr(), n, idx.data_ptr(),
+                                 cnt.data_ptr(), y.data_ptr(), n, 0, ws.data_ptr(), ws.numel(), ctypes.byref(pl),
+                                 _stream_handle(dev))
+        assert rc == _lib.BSG_OK, _lib.last_error()
+        torch.cuda.synchronize()
+        assert not bool((ws[256:sel] == 0xAB).all()), f"bt={bt} K={kdim}: no score launch"
+        want = orc.select_topk_l1(x, k)
+        assert np.array_equal(idx.cpu().numpy(), want)
+        assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), f"two-launch bt={bt} K={kdim}")
+
+
 def test_select_density_wrapper(dev):
     x = np.random.default_rng(9).normal(0, 1, size=(64, 4096)).astype(np.float16)
     got = bsa._select_active_blocks_l1(to_dev(x, dev).view(64, 1, 4096), 0.48)

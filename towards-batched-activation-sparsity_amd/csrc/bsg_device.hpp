@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "bsgemm.h"
 
 namespace bsgk {
@@ -120,10 +122,13 @@ constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, 
 #define BSG_TL_END(p, stored_y) ((void)0)
 #endif
 
-enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2, MODE_TOPK = 3 };
+// MODE_TOPK: the GEMM ranks block scores an earlier launch wrote.  MODE_TOPK_SELF: every
+// work-group also computes those scores itself from x (fp16, at most BSG_SELF_MAX_ROWS rows).
+enum { MODE_LIST = 0, MODE_BITMAP = 1, MODE_DENSE = 2, MODE_TOPK = 3, MODE_TOPK_SELF = 4 };
 // A GEMM ranks block scores itself (MODE_TOPK) up to this many blocks: keys and ranks fit its
 // block-list buffer, and a one-wave work-group flags at most 8 per thread.
 #define BSG_TOPK_MAX_NBLK 512
+#define BSG_SELF_MAX_ROWS 8
 
 // Kind 3 activation staging: 1 KiB loads per wave, and the LDS it may take.
 #define BSG_FMA_X_LOADS 16
@@ -264,12 +269,13 @@ __device__ __forceinline__ void pad_scores(S* s_sc, int nb) {
 // barriers lie between), so emit may overwrite them.
 template <int NT, typename Emit>
 __device__ __forceinline__ int topk_l1_list(const uint64_t* scores, int nb, int k, bool keyed, uint64_t* s_key,
-                                            int* s_rank, int* s_scan, Emit emit) {
+                                            int* s_rank, int* s_scan, Emit emit, bool staged = false) {
   constexpr int W = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nb16 = (nb + 15) & ~15;
-  for (int i = tid; i < nb16; i += NT) {
+  // staged: s_key already holds the keys and pads (self_score_keys)
+  for (int i = tid; !staged && i < nb16; i += NT) {
     uint64_t key = 0;  // pads: lowest score, ids >= nb, never ahead
     if (i < nb) {
       const uint64_t v = scores[i];
@@ -396,6 +402,115 @@ __device__ __forceinline__ bool tile_columns(const GemmParams& p, int tile, int 
   return true;
 }
 
+// |x| of an fp16 value in units of 2^-24 (exact for every finite value; Inf/NaN map above
+// every finite value, NaN above Inf).
+__device__ __forceinline__ uint64_t f16_units(uint32_t hbits) {
+  const uint32_t b = hbits & 0x7fffu;
+  const uint32_t e = b >> 10, m = b & 0x3ffu;
+  return e == 0 ? (uint64_t)m : ((uint64_t)(1024u | m) << (e - 1));
+}
+
+__device__ __forceinline__ uint64_t f16x8_units(u32x4 v) {
+  return f16_units(v.x & 0xffffu) + f16_units(v.x >> 16) + f16_units(v.y & 0xffffu) + f16_units(v.y >> 16) +
+         f16_units(v.z & 0xffffu) + f16_units(v.z >> 16) + f16_units(v.w & 0xffffu) + f16_units(v.w >> 16);
+}
+
+// sum |x| of 8 fp16 values as an fp64 value, exactly: every finite |x| is a multiple of 2^-24
+// below 2^16, so every partial sum of up to 512 of them needs at most 50 significant bits and
+// fp64 adds are exact.  A group holding Inf or NaN takes the integer units of f16x8_units (their
+// mapping above every finite value), scaled by 2^-24 (exact), so either way the result times
+// 2^24 is the integer sum of the units.
+__device__ __forceinline__ double f16x8_abs_sum(u32x4 v) {
+  auto nonfinite = [](uint32_t d) {  // a 16-bit half of d with exponent 31
+    const uint32_t t = (d & 0x7c007c00u) ^ 0x7c007c00u;
+    return ((t - 0x00010001u) & ~t & 0x80008000u) != 0u;
+  };
+  if (nonfinite(v.x) | nonfinite(v.y) | nonfinite(v.z) | nonfinite(v.w))
+    return (double)f16x8_units(v) * 0x1p-24;
+  auto h = [](uint32_t d, int hi) {
+    return fabs((double)(float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? d >> 16 : d & 0xffffu)));
+  };
+  return ((h(v.x, 0) + h(v.x, 1)) + (h(v.y, 0) + h(v.y, 1))) + ((h(v.z, 0) + h(v.z, 1)) + (h(v.w, 0) + h(v.w, 1)));
+}
+
+// One DPP row shift (row_shr:n = 0x110 + n) of a 64-bit value: lane i of each 16-lane row
+// reads lane i - n of the same row, and 0 where that lane lies outside the row.
+template <int CTRL>
+__device__ __forceinline__ uint64_t u64_row_shr(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, CTRL, 0xf, 0xf, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), CTRL, 0xf, 0xf, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// The 64-bit value of lane `src` of the wave.
+__device__ __forceinline__ uint64_t u64_lane(uint64_t x, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)x, src, 64);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(x >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// MODE_TOPK_SELF: the exact-L1 score of every K-block of x[0, bt) (bt <= BSG_SELF_MAX_ROWS, fp16)
+// computed by this work-group alone -- the integers bsg_score_l1_kernel writes: block j sums
+// |x| over the rows and its channels in units of 2^-24 -- as top-k keys in s_key[0, nb16) (keyed
+// order as topk_l1_list builds it, pads 0).  A segment of SEG = 8 x (rows rounded up to a power
+// of two) consecutive lanes covers one block (lane s of the segment: row s / 8, channels
+// 8 (s % 8) .. +7), so a pass of the work-group covers NT / SEG blocks.  The loads of up to U
+// passes are in flight before any is summed; passes past the last block are skipped (a
+// work-group-uniform test).  Segment sums: DPP row shifts give the sum of the 8 or 16 lanes up
+// to each lane of a 16-lane row, and for 32- and 64-lane segments the last lane adds the other
+// rows' totals.  x is read from L2 (every work-group of the launch reads the same bytes).
+// Ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void self_score_keys(const GemmParams& p, uint64_t* s_key) {
+  constexpr int U = 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int rp2 = p.bt <= 1 ? 1 : p.bt <= 2 ? 2 : p.bt <= 4 ? 4 : 8;
+  const int seg = 8 * rp2;  // 8, 16, 32 or 64 lanes
+  const int per_pass = NT / seg;
+  const int s = tid % seg, row = s >> 3, grp = s & 7;
+  const int nb = p.nblk, nb16 = (nb + 15) & ~15;
+  const uint16_t* x = (const uint16_t*)p.x;
+  for (int j0 = 0; j0 < nb; j0 += U * per_pass) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + u * per_pass + tid / seg;
+      const int col = 64 * j + 8 * grp;
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (row < p.bt && j < nb && col < p.K) v[u] = *(const u32x4*)(x + (size_t)row * (size_t)p.ldx + col);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + u * per_pass >= nb) break;  // uniform: no block in this pass or the next
+      // exact fp64 sums (f16x8_abs_sum); the DPP steps move their bit patterns
+      auto shr = [](double a, auto ctrl) {
+        return a + __builtin_bit_cast(double, u64_row_shr<decltype(ctrl)::value>(__builtin_bit_cast(uint64_t, a)));
+      };
+      double a = f16x8_abs_sum(v[u]);
+      a = shr(a, std::integral_constant<int, 0x111>{});
+      a = shr(a, std::integral_constant<int, 0x112>{});
+      a = shr(a, std::integral_constant<int, 0x114>{});
+      if (seg >= 16) a = shr(a, std::integral_constant<int, 0x118>{});  // lane 15 of a row: its total
+      if (seg >= 32) {
+        const double r1 = __builtin_bit_cast(  // the previous row's total
+            double, u64_lane(__builtin_bit_cast(uint64_t, a), ((lane | 15) - 16) & 63));
+        if (lane & 16) a += r1;  // lanes 31, 63: their halves
+      }
+      if (seg == 64) {
+        const double h = __builtin_bit_cast(double, u64_lane(__builtin_bit_cast(uint64_t, a), 31));
+        if (lane == 63) a += h;
+      }
+      const int j = j0 + u * per_pass + tid / seg;
+      if (s == seg - 1 && j < nb) {
+        const uint64_t units = (uint64_t)(a * 0x1p24);  // an integer below 2^50: exact
+        s_key[j] = p.keyed ? (units << 11) | (uint64_t)(BSG_MAX_NBLK - 1 - j) : units;
+      }
+    }
+  }
+  if (tid < nb16 - nb) s_key[nb + tid] = 0;  // pads: lowest score, never ahead
+  __syncthreads();
+}
+
 // The first na block ids in ascending order, into s_ids[0, na) (na <= BSG_MAX_NBLK / 2): the
 // sequence an ascending sort of the list gives (equal ids are equal, so their order does not
 // show).  The ids go to LDS as unsigned keys 0x7fffffff - id (descending in the id).  A list that
@@ -435,24 +550,28 @@ __device__ __forceinline__ void sort_block_list(const int32_t* ids, int na, int*
 // Stage this call's active-block list in LDS (list copy, bitmap compaction, top-k of block
 // scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
 // and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
-// second (up to 512 blocks).  SORT: the list may be sorted here (p.sort_list, a 1-D list launch
-// only; the 2-D forms are compiled without it).
-template <int NT, bool SORT>
+// second (up to 512 blocks).  ONE_D: the in-kernel sort of a 1-D list (p.sort_list) is compiled
+// in (the 2-D forms have none); SELF: the self-scored top-k (MODE_TOPK_SELF) is (1-D forms of
+// the MFMA kinds only).
+template <int NT, bool ONE_D, bool SELF = ONE_D>
 __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
   const int tid = threadIdx.x;
   int na;
-  if (p.mode == MODE_TOPK) {
+  if (p.mode == MODE_TOPK || (SELF && p.mode == MODE_TOPK_SELF)) {
     // Every work-group ranks the scores itself (identically), so the list needs no other
     // launch; keys and ranks are staged in the list buffer and overwritten by the kept ids.
+    // MODE_TOPK_SELF computes the scores here too, so the selection needs no launch of its own.
+    const bool self = SELF && p.mode == MODE_TOPK_SELF;
+    if (self) self_score_keys<NT>(p, (uint64_t*)s_ids);
     na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
-                          s_scan, [&](int pos, int id) { s_ids[pos] = id; });
+                          s_scan, [&](int pos, int id) { s_ids[pos] = id; }, self);
   } else if (p.mode == MODE_LIST) {
     na = p.na;
     if (p.na_dev != nullptr) {
       const int d = *p.na_dev;
       na = d < 0 ? 0 : (d < na ? d : na);
     }
-    if (SORT && p.sort_list)
+    if (ONE_D && p.sort_list)
       sort_block_list<NT>(p.idx, __builtin_amdgcn_readfirstlane(na), s_ids);
     else
       for (int i = tid; i < na; i += NT) s_ids[i] = p.idx[i];
@@ -473,7 +592,8 @@ __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids,
   }
   na = __builtin_amdgcn_readfirstlane(na);
   __syncthreads();
-  if (p.mode == MODE_TOPK && p.idx_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+  if ((p.mode == MODE_TOPK || p.mode == MODE_TOPK_SELF) && p.idx_out != nullptr && blockIdx.x == 0 &&
+      blockIdx.y == 0) {
     for (int i = tid; i < na; i += NT) p.idx_out[i] = s_ids[i];
     if (tid == 0) *p.na_out = na;
   }
@@ -936,7 +1056,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D, false>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * w) / WPG);
   const int pend = (int)(((int64_t)na * (w + 1)) / WPG);

@@ -40,6 +40,16 @@
 
 // The GEMM ranks the block scores itself (MODE_TOPK) when each of its waves has at most this many
 // rank items (64 blocks x 16 scores each); otherwise a separate rank launch runs first.
+// The GEMM scores the blocks itself as well (one launch for the whole selection + GEMM) when
+// the activations every work-group reads for that, bt x K x 2 bytes, are at most this many bytes
+// (and bt <= BSG_SELF_MAX_ROWS).  Measured (selection + GEMM per call, graph of rotated launches,
+// s=0.5): one launch saves 1.5 / 1.0 us at q/k/v/o B=1 / 2, 1.6 / 0.8 us at gate/up and 1.0 us at
+// down B=1 (22 KiB); at 32 KiB (B=4, K=4096) it loses 0.3-0.4 us, since the wait for x grows
+// with the bytes while the two-launch cost (a score launch and a cold load of its scores) stays.
+#ifndef BSG_SELF_SCORE_MAX_X_BYTES
+#define BSG_SELF_SCORE_MAX_X_BYTES 24576
+#endif
+
 #ifndef BSG_TOPK_ITEMS_PER_WAVE
 #define BSG_TOPK_ITEMS_PER_WAVE 12
 #endif
@@ -304,14 +314,6 @@ __global__ __launch_bounds__(256) void bsg_zero_kernel(uint32_t* __restrict__ p,
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
 }
 
-// |x| of an fp16 value in units of 2^-24 (exact for every finite value; Inf/NaN map above
-// every finite value, NaN above Inf).
-__device__ __forceinline__ uint64_t f16_units(uint32_t hbits) {
-  const uint32_t b = hbits & 0x7fffu;
-  const uint32_t e = b >> 10, m = b & 0x3ffu;
-  return e == 0 ? (uint64_t)m : ((uint64_t)(1024u | m) << (e - 1));
-}
-
 struct SelParams {
   const uint16_t* x;
   int64_t ldx;
@@ -325,14 +327,6 @@ struct SelParams {
 // integer units, and stores it.  The ranking (bsg_rank_l1_kernel, or a GEMM in top-k mode) is a
 // separate launch: a last-arriver hand-off would put every work-group's increment on one
 // device-scope counter, and those serialize (4-7 us at 64-172 blocks, measured).
-// One DPP row shift (row_shr:n = 0x110 + n) of a 64-bit value: lane i of each 16-lane row
-// reads lane i - n of the same row, and 0 where that lane lies outside the row.
-template <int CTRL>
-__device__ __forceinline__ uint64_t u64_row_shr(uint64_t x) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, CTRL, 0xf, 0xf, true);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), CTRL, 0xf, 0xf, true);
-  return ((uint64_t)hi << 32) | lo;
-}
 
 __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
   __shared__ uint64_t s_part[16];
@@ -355,10 +349,7 @@ __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
       if (gi < groups && col < p.K) v[u] = *(const u32x4*)(p.x + (size_t)row * (size_t)p.ldx + col);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      acc += f16_units(v[u].x & 0xffffu) + f16_units(v[u].x >> 16) + f16_units(v[u].y & 0xffffu) +
-             f16_units(v[u].y >> 16) + f16_units(v[u].z & 0xffffu) + f16_units(v[u].z >> 16) +
-             f16_units(v[u].w & 0xffffu) + f16_units(v[u].w >> 16);
+    for (int u = 0; u < U; ++u) acc += f16x8_units(v[u]);
   }
   // Inclusive scan within each 16-lane row (a few cycles per step, no LDS round trip): lane 15
   // of every row ends with the row's sum; the 16 row sums of the work-group meet in LDS.
@@ -726,8 +717,13 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
     if (na > 0 && !idx) return fail(BSG_ERR_ARG, "active_blocks is null");
     if (ex.sort_list && na > BSG_MAX_NBLK / 2)
       return fail(BSG_ERR_UNSUPPORTED, "in-kernel sort: num_active=%d (at most %d)", na, BSG_MAX_NBLK / 2);
-  } else if (mode == MODE_TOPK) {
-    if (!ex.scores || na < 0) return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)ex.scores, na);
+  } else if (mode == MODE_TOPK || mode == MODE_TOPK_SELF) {
+    if (mode == MODE_TOPK && !ex.scores)
+      return fail(BSG_ERR_ARG, "top-k: scores=%p k=%d", (const void*)ex.scores, na);
+    if (na < 0) return fail(BSG_ERR_ARG, "top-k: k=%d", na);
+    if (mode == MODE_TOPK_SELF && (bt > BSG_SELF_MAX_ROWS || dtype != BSG_F16 || ex.nidx != nullptr))
+      return fail(BSG_ERR_UNSUPPORTED, "self-scored top-k: bt=%lld dtype=%d (fp16, at most %d rows, 1-D)",
+                  (long long)bt, dtype, BSG_SELF_MAX_ROWS);
     if (nblk > BSG_TOPK_MAX_NBLK)
       return fail(BSG_ERR_UNSUPPORTED, "top-k in the GEMM: %d blocks (at most %d)", nblk, BSG_TOPK_MAX_NBLK);
     if (na > nblk) na = nblk;
@@ -745,6 +741,8 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   // a 2-D launch fills the chip with its active blocks only
   rc = resolve(bt, ex.nidx != nullptr ? (int64_t)ex.nn * 64 : N, nblk, na, cu, &pl);
   if (rc != BSG_OK) return rc;
+  if (mode == MODE_TOPK_SELF && pl.kind == KIND_FMA)
+    return fail(BSG_ERR_UNSUPPORTED, "self-scored top-k: not in kind 3");
   const int64_t need = gemm_ws_bytes(bt, N, &pl);
   const bool fixed_ws = ex.part_fixed != nullptr;
   if (fixed_ws) {
@@ -1180,7 +1178,20 @@ static int select_gemm_run(const void* x, int64_t ldx, int64_t bt, int64_t K, in
   // the rank launch that 8 forced).  Otherwise a
   // one-work-group rank launch (about 3 us) is cheaper than ranking in each work-group.
   const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
-  if (nblk <= BSG_TOPK_MAX_NBLK && items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group) {
+  const bool rank_in_gemm =
+      nblk <= BSG_TOPK_MAX_NBLK && items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group;
+  if (rank_in_gemm && bt <= BSG_SELF_MAX_ROWS && bt * K * 2 <= BSG_SELF_SCORE_MAX_X_BYTES && pl.kind != KIND_FMA) {
+    // One launch: every GEMM work-group scores the blocks from x itself, ranks them and walks
+    // the kept list; no score buffer is written.
+    rc = select_l1_check(x, ldx, bt, K, k, idx_out, na_out, dtype);
+    if (rc != BSG_OK) return rc;
+    LaunchExtras ex = fx;
+    ex.idx_out = idx_out;
+    ex.na_out = na_out;
+    return launch_gemm(MODE_TOPK_SELF, x, ldx, bt, K, wp, N, nullptr, k, nullptr, nullptr, 0, y, ldy, dtype, gws,
+                       gws_bytes, &pl, stream, ex);
+  }
+  if (rank_in_gemm) {
     // Two launches: the block scores, then the GEMM, whose work-groups each rank them and walk
     // the kept list (work-group (0, 0) also publishes it).
     rc = select_l1_run(x, ldx, bt, K, k, idx_out, na_out, dtype, scores, stream, false);
