@@ -73,3 +73,33 @@ def test_graph_select_gemm(dev):
                                                   count_out=cnt_buf), out)
     assert int(cnt_buf.item()) == 31
     assert np.all(np.diff(idx_buf.cpu().numpy()) > 0)
+
+
+def test_graph_dropin_with_in_kernel_sort(dev):
+    """The reference's runtime entry with an unsorted list (sorted inside the GEMM's staging)
+    captured and replayed: every replay and every eager call in between equal the first eager
+    result bit for bit."""
+    bt, k, n, na = 16, 11008, 4096, 86
+    x, w_nk, idx = case(24, bt, k, n, na)
+    xt = to_dev(x, dev).view(bt, 1, k)
+    wt = to_dev(w_nk, dev)
+    it = to_dev(np.random.default_rng(3).permutation(idx).astype(np.int32), dev)
+    out = torch.empty(bt, 1, n, dtype=torch.float16, device=dev)
+    _replays_match(lambda: bsa._prepacked_block_sparse_gemm_from_active_blocks(
+        xt, wt, it, out, cache_prefix="graph_sort"), out)
+
+
+def test_graph_one_launch_select_gemm(dev):
+    """Selection + GEMM at B=2 (the GEMM scores the blocks itself: one launch) in a graph."""
+    bt, k, n = 2, 4096, 4096
+    x, w_nk, _ = case(25, bt, k, n, 1, "normal")
+    xt = to_dev(x, dev).view(bt, 1, k)
+    wt = to_dev(w_nk, dev)
+    out = torch.empty(bt, 1, n, dtype=torch.float16, device=dev)
+    idx_buf = torch.empty(13, dtype=torch.int32, device=dev)
+    cnt_buf = torch.empty(1, dtype=torch.int32, device=dev)
+    _replays_match(lambda: bsa.select_sparse_gemm(xt, wt, out, 13, cache_prefix="graph_sel1", idx_out=idx_buf,
+                                                  count_out=cnt_buf), out)
+    assert int(cnt_buf.item()) == 13
+    from oracle import bsg_oracle as orc
+    assert np.array_equal(idx_buf.cpu().numpy(), orc.select_topk_l1(x, 13))
