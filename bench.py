@@ -25,7 +25,8 @@ cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host
 
 The same line also carries, measured in the same run after the matrix (skip with --no-extras):
 fused_select_gemm = configs[3] (exact-L1 select k=31 of 64 + gate/up GEMM at B=64, indices
-checked bit-exact), decode_step = configs[4] (the 32-layer decode step of linears as one
+checked bit-exact), fused_select_gemm_b2 = the same call at q/k/v/o B=2 k=32 (one launch: the
+GEMM scores the blocks itself), decode_step = configs[4] (the 32-layer decode step of linears as one
 hipGraph), eager_calls = the host cost of one eager call of the drop-in entry points (what
 the model patch pays per linear layer), perstep_replay = the reference's headline table (its
 per-step sparsity maps of the 224-GEMM decode step) at B=2, 4, 8, 16, 32, 64.
@@ -611,6 +612,9 @@ def run_matrix(args, dev):
         log("configs[3]: fused exact-L1 select + GEMM ...")
         extras["fused_select_gemm"] = measure_fused(args, dev)
         log(f"configs[3] done ({time.perf_counter() - t0:.1f} s): {extras['fused_select_gemm']['us_select_plus_gemm']} us")
+        extras["fused_select_gemm_b2"] = measure_fused(args, dev, shape="qkvo", bt=2, keep=32)
+        log(f"select + GEMM at q/k/v/o B=2: {extras['fused_select_gemm_b2']['us_select_plus_gemm']} us "
+            f"(GEMM alone {extras['fused_select_gemm_b2']['us_gemm_only']} us)")
         log("configs[4]: 32-layer decode step ...")
         extras["decode_step"] = measure_decode(args, dev)
         log(f"configs[4] done ({time.perf_counter() - t0:.1f} s): {extras['decode_step']['ms_per_step']} ms/step")
@@ -844,10 +848,12 @@ def measure_eager(args, dev):
     return res
 
 
-def measure_fused(args, dev):
-    """fused exact-L1 selection (k=31 of 64) + sparse GEMM on gate/up at B=64
-    (K=4096 -> N=11008), rotated over >= 1 GiB of distinct active weight; indices checked
-    bit-exact against the oracle first.  Returns the measured fields."""
+def measure_fused(args, dev, shape="gate_up", bt=64, keep=31):
+    """BASELINE config 4 (the defaults): fused exact-L1 selection (k=31 of 64) + sparse GEMM on
+    gate/up at B=64 (K=4096 -> N=11008), rotated over >= 1 GiB of distinct active weight; indices
+    checked bit-exact against the oracle first.  Other (shape, bt, keep) measure the same call
+    elsewhere (at bt <= 8 and bt x K x 2 <= 24 KiB it is one launch).  Returns the measured
+    fields."""
     import numpy as np
     import torch
 
@@ -855,10 +861,9 @@ def measure_fused(args, dev):
     from bsa_mi355x.select import select_gemm_packed
     from oracle import bsg_oracle as orc
 
-    bt, keep = 64, 31
-    k, n = SHAPES["gate_up"]
-    pool = ShapePool("gate_up", k, n, dev, copies_for(keep * 64 * n * 2))
-    pt = Point("gate_up_b64_fused", pool, bt, keep, dev)
+    k, n = SHAPES[shape]
+    pool = ShapePool(shape, k, n, dev, copies_for(keep * 64 * n * 2))
+    pt = Point(f"{shape}_b{bt}_fused", pool, bt, keep, dev)
     idx = torch.empty(keep, dtype=torch.int32, device=dev)
     cnt = torch.empty(1, dtype=torch.int32, device=dev)
     select_gemm_packed(pt.x, pool.packed[0], n, keep, pt.y, idx_out=idx, count_out=cnt, workspace_prefix="fused_bench")
@@ -871,14 +876,17 @@ def measure_fused(args, dev):
     if not orc.within_tolerance(pt.y.float().cpu().numpy(), y_ref):
         raise SystemExit("fused select+GEMM output outside tolerance")
     log("fused: indices bit-exact, GEMM within tolerance")
-    plan = bsa.resolve_plan(bt, n, pt.nblk, keep, dev)
+    # each call with its own tuned plan: the selection + GEMM entry, and the plain GEMM's
+    plan = bsa.resolve_plan(bt, n, pt.nblk, keep, dev, select=True)
+    plan_gemm = bsa.resolve_plan(bt, n, pt.nblk, keep, dev)
 
     def fused(i):
         return lambda: select_gemm_packed(pt.x, pool.packed[i], n, keep, pt.y, plan=plan, idx_out=idx, count_out=cnt,
                                           workspace_prefix="fused_bench")
 
     def gemm_only(i):
-        return lambda: bsa.gemm_packed(pt.x, pool.packed[i], n, idx, pt.y, plan=plan, workspace_prefix="fused_gemm")
+        return lambda: bsa.gemm_packed(pt.x, pool.packed[i], n, idx, pt.y, plan=plan_gemm,
+                                       workspace_prefix="fused_gemm")
 
     def select_only(i):
         return lambda: bsa.select_topk_l1(pt.x, keep, idx_out=idx, count_out=cnt, workspace_prefix="fused_sel")
@@ -894,11 +902,13 @@ def measure_fused(args, dev):
         cpu_us = cpu_select_gemm_us(pt.x_np, pool.w_kn_np, keep)
         cpu = {"cpu_us_select_plus_gemm": round(cpu_us, 1), "cpu_cores": len(os.sched_getaffinity(0)),
                "gpu_speedup_over_cpu": round(cpu_us / t_fused, 1)}
-    out = {"workload": "fused exact-L1 select (k=31 of 64) + sparse GEMM, gate/up B=64 K=4096 N=11008 (configs[3])",
+    out = {"workload": f"fused exact-L1 select (k={keep} of {pt.nblk}) + sparse GEMM, {shape} B={bt} K={k} N={n}"
+                       + (" (configs[3])" if (shape, bt, keep) == ("gate_up", 64, 31) else
+                          " (one launch: the GEMM scores the blocks itself)" if bt <= 8 and bt * k * 2 <= 24576 else ""),
            "us_select_plus_gemm": round(t_fused, 3), "us_gemm_only": round(t_gemm, 3),
            "us_select_only": round(t_sel, 3), "select_overhead_us": round(t_fused - t_gemm, 3),
            "GBps_active": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-           "plan": list(plan.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True,
+           "plan": list(plan.as_tuple()), "plan_gemm_only": list(plan_gemm.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True,
            **cpu}
     del pool, pt
     torch.cuda.empty_cache()

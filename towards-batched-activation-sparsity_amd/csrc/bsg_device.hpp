@@ -50,9 +50,11 @@ typedef void (*GemmFn)(GemmParams);
 enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4, KIND_VT = 5, KIND_VT1 = 6 };
 
 // 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
+// f16_self: the fp16 form compiled with the self-scored top-k (MODE_TOPK_SELF), for the 16-row
+// tiles of the MFMA kinds (null elsewhere); the other forms leave that code out.
 struct KernelEntry {
   int kind, rows, nsub, wpg, depth;
-  GemmFn f16, bf16, f16_2d, bf16_2d;
+  GemmFn f16, bf16, f16_2d, bf16_2d, f16_self;
 };
 
 // A translation unit's slice of the instantiated tile set.
@@ -551,9 +553,9 @@ __device__ __forceinline__ void sort_block_list(const int32_t* ids, int na, int*
 // scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
 // and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
 // second (up to 512 blocks).  ONE_D: the in-kernel sort of a 1-D list (p.sort_list) is compiled
-// in (the 2-D forms have none); SELF: the self-scored top-k (MODE_TOPK_SELF) is (1-D forms of
-// the MFMA kinds only).
-template <int NT, bool ONE_D, bool SELF = ONE_D>
+// in (the 2-D forms have none); SELF: the self-scored top-k (MODE_TOPK_SELF) is (the f16_self
+// instantiations only).
+template <int NT, bool ONE_D, bool SELF = false>
 __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
   const int tid = threadIdx.x;
   int na;
@@ -706,7 +708,7 @@ __device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_l
 // the work-group's share of the block list into contiguous slices and are reduced through LDS
 // in wave order.  Each wave loads its own X fragments.  Best when bt is small (the X fragments
 // are few) and many narrow column tiles are needed to fill the chip.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D>
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D, bool SELF = false>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
   constexpr int F = BTT * NSUB;
@@ -729,7 +731,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D, SELF>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // This wave's contiguous slice [pbeg, pend) of the list.
@@ -868,7 +870,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
 // (WK = 2): 2*WC waves, column group x 32-channel half of every block, so each wave issues half
 // the MFMAs and LDS reads of a block and two waves share each SIMD, overlapping one wave's
 // barrier and LDS waits with the other's MFMAs; the halves are summed through LDS at the end.
-template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D>
+template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D, bool SELF = false>
 __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p) {
   constexpr int WPG = WC * WK;
   constexpr int NT = 64 * WPG;
@@ -895,7 +897,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D, SELF>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // The work-group's contiguous slice of the list (all its waves walk it together).
@@ -1056,7 +1058,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_fma_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D, false>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * w) / WPG);
   const int pend = (int)(((int64_t)na * (w + 1)) / WPG);
@@ -1243,7 +1245,7 @@ __device__ __forceinline__ void vt_columns(int t, int G, int T, int* first, int*
 // KH = 1 (kind 6): no channel-half split; each of the WB waves loads both halves of every
 // weight subtile and activation row tile of its blocks (the two halves of an activation row are
 // one 128-byte line, requested back to back by one wave).
-template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2>
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SELF = false>
 __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p) {
   constexpr int NW = KH * WB;
   constexpr int NT = 64 * NW;
@@ -1265,7 +1267,7 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, true>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, true, SELF>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * b) / WB);
   const int pend = (int)(((int64_t)na * (b + 1)) / WB);
@@ -1382,25 +1384,45 @@ constexpr GemmFn kernel_2d() {
   }
 }
 
+// The self-scoring fp16 form of a 16-row tile of the MFMA kinds, or null (other row counts:
+// the self-scored selection runs at most 8 rows).
+template <int KIND, int B, int S, int W, int D>
+constexpr GemmFn kernel_self() {
+  if constexpr (B != 1) {
+    return nullptr;
+  } else if constexpr (KIND == KIND_KSPLIT) {
+    return bsg_gemm_kernel<_Float16, B, S, W, D, false, true>;
+  } else if constexpr (KIND == KIND_XLDS) {
+    return bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false, true>;
+  } else if constexpr (KIND == KIND_XLDS_KH) {
+    return bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false, true>;
+  } else if constexpr (KIND == KIND_VT) {
+    return bsg_gemm_vt_kernel<_Float16, B, S, W / 2, D, 2, true>;
+  } else {
+    return bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, true>;
+  }
+}
+
 #define BSG_K(B, S, W, D)                                                                                          \
   {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D, false>, bsg_gemm_kernel<__bf16, B, S, W, D, false>, \
-   kernel_2d<KIND_KSPLIT, _Float16, B, S, W, D>(), kernel_2d<KIND_KSPLIT, __bf16, B, S, W, D>()}
+   kernel_2d<KIND_KSPLIT, _Float16, B, S, W, D>(), kernel_2d<KIND_KSPLIT, __bf16, B, S, W, D>(),                   \
+   kernel_self<KIND_KSPLIT, B, S, W, D>()}
 #define BSG_X(B, S, W, D)                                                                     \
   {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false>,           \
    bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D, false>, kernel_2d<KIND_XLDS, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>()}
+   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>(), kernel_self<KIND_XLDS, B, S, W, D>()}
 #define BSG_Y(B, S, W, D)                                                                        \
   {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false>,        \
    bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D, false>, kernel_2d<KIND_XLDS_KH, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>()}
+   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>(), kernel_self<KIND_XLDS_KH, B, S, W, D>()}
 #define BSG_V(B, S, W, D)                                                                               \
   {KIND_VT, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W / 2, D>, bsg_gemm_vt_kernel<__bf16, B, S, W / 2, D>, \
-   nullptr, nullptr}
+   nullptr, nullptr, kernel_self<KIND_VT, B, S, W, D>()}
 #define BSG_V1(B, S, W, D)                                                                                \
   {KIND_VT1, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1>, bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1>, \
-   nullptr, nullptr}
+   nullptr, nullptr, kernel_self<KIND_VT1, B, S, W, D>()}
 #define BSG_F(R, S, W, D)                                                                                 \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
-   kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>()}
+   kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>(), nullptr}
 
 }  // namespace

@@ -741,8 +741,6 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   // a 2-D launch fills the chip with its active blocks only
   rc = resolve(bt, ex.nidx != nullptr ? (int64_t)ex.nn * 64 : N, nblk, na, cu, &pl);
   if (rc != BSG_OK) return rc;
-  if (mode == MODE_TOPK_SELF && pl.kind == KIND_FMA)
-    return fail(BSG_ERR_UNSUPPORTED, "self-scored top-k: not in kind 3");
   const int64_t need = gemm_ws_bytes(bt, N, &pl);
   const bool fixed_ws = ex.part_fixed != nullptr;
   if (fixed_ws) {
@@ -814,7 +812,11 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
 
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
-  GemmFn fn = ex.nidx != nullptr ? (dtype == BSG_F16 ? ke->f16_2d : ke->bf16_2d) : (dtype == BSG_F16 ? ke->f16 : ke->bf16);
+  GemmFn fn = mode == MODE_TOPK_SELF ? ke->f16_self
+              : ex.nidx != nullptr ? (dtype == BSG_F16 ? ke->f16_2d : ke->bf16_2d)
+                                   : (dtype == BSG_F16 ? ke->f16 : ke->bf16);
+  if (fn == nullptr && mode == MODE_TOPK_SELF)
+    return fail(BSG_ERR_UNSUPPORTED, "self-scored top-k: no instantiation for this tile (16-row MFMA tiles only)");
   if (fn == nullptr) return fail(BSG_ERR_UNSUPPORTED, "2-D: no instantiation for this tile");
   // Kind 3: LDS for the staged activations of the whole list (na is the list capacity; a
   // device-side count or a bitmap only shortens it).
@@ -1180,7 +1182,9 @@ static int select_gemm_run(const void* x, int64_t ldx, int64_t bt, int64_t K, in
   const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
   const bool rank_in_gemm =
       nblk <= BSG_TOPK_MAX_NBLK && items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group;
-  if (rank_in_gemm && bt <= BSG_SELF_MAX_ROWS && bt * K * 2 <= BSG_SELF_SCORE_MAX_X_BYTES && pl.kind != KIND_FMA) {
+  const KernelEntry* ke = find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
+  if (rank_in_gemm && bt <= BSG_SELF_MAX_ROWS && bt * K * 2 <= BSG_SELF_SCORE_MAX_X_BYTES && ke != nullptr &&
+      ke->f16_self != nullptr) {
     // One launch: every GEMM work-group scores the blocks from x itself, ranks them and walks
     // the kept list; no score buffer is written.
     rc = select_l1_check(x, ldx, bt, K, k, idx_out, na_out, dtype);
