@@ -210,9 +210,6 @@ __device__ __forceinline__ int wg_exclusive_scan(int v, int* scratch, int* total
   return base + incl - v;
 }
 
-// The one-work-group top-k (1024 threads) flags at most 2 blocks per thread (kept flags: one
-// 32-bit mask per thread).
-static_assert(BSG_MAX_NBLK <= 32 * 1024, "selector chunk layout");
 
 // Rank of block j among nb scores in LDS, ordered (score desc, block id asc): the number of
 // blocks ahead of it.  s_sc holds the nb scores followed by zeros up to a multiple of 16 (a pad
@@ -265,13 +262,12 @@ __device__ __forceinline__ void pad_scores(S* s_sc, int nb) {
 // is a unique key in the same order and one compare decides.  The nb^2 compares are spread over
 // every wave of the work-group: a work item is (64 blocks, 16 scores), each lane counts the
 // scores ahead of its block and adds the count to the block's rank in LDS.  s_key holds nb
-// keys rounded up to 16, s_rank nb ints; each thread then flags a contiguous chunk of at most
-// 32 blocks (nb <= 32 * NT), so a scan of the counts gives ascending positions.  Returns
-// min(k, nb).  Every thread has finished reading s_key and s_rank when emit runs (the scan's
-// barriers lie between), so emit may overwrite them.
+// keys rounded up to 16, s_rank nb ints; per-wave ballots of the kept flags then give ascending
+// positions.  Returns min(k, nb).  No thread reads s_key after the ranking barrier, so emit may
+// overwrite s_key (not s_rank, which waves still read while others emit).
 template <int NT, typename Emit>
 __device__ __forceinline__ int topk_l1_list(const uint64_t* scores, int nb, int k, bool keyed, uint64_t* s_key,
-                                            int* s_rank, int* s_scan, Emit emit, bool staged = false) {
+                                            int* s_rank, Emit emit, bool staged = false) {
   constexpr int W = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -309,23 +305,20 @@ __device__ __forceinline__ int topk_l1_list(const uint64_t* scores, int nb, int 
     if (j < nb && r != 0) atomicAdd(&s_rank[j], r);
   }
   __syncthreads();
-  const int per = (nb + NT - 1) / NT;
-  const int beg = tid * per < nb ? tid * per : nb;
-  const int end = beg + per < nb ? beg + per : nb;
+  // Ascending positions of the kept blocks (rank < kk) without a scan: every wave ballots the
+  // kept flags of each 64-block group in turn and keeps the running count, so the position of
+  // block j is the kept count before its group plus the kept lanes below it; wave g % W emits
+  // group g.  No barrier, and the only LDS reads are of s_rank.
   const int kk = k < nb ? k : nb;
-  uint32_t selmask = 0;
-  int c = 0;
+  int before = 0;
 #pragma unroll 1
-  for (int q = 0; q < end - beg; ++q)
-    if (s_rank[beg + q] < kk) {
-      selmask |= 1u << q;
-      ++c;
-    }
-  int total = 0;
-  int o = wg_exclusive_scan<NT>(c, s_scan, &total);
-#pragma unroll 1
-  for (int q = 0; q < end - beg; ++q)
-    if ((selmask >> q) & 1u) emit(o++, beg + q);
+  for (int g = 0; 64 * g < nb; ++g) {
+    const int j = 64 * g + lane;
+    const bool keep = j < nb && s_rank[j] < kk;
+    const uint64_t m = __ballot(keep);
+    if (g % W == w && keep) emit(before + __popcll(m & ((1ull << lane) - 1ull)), j);
+    before += __popcll(m);
+  }
   return kk;
 }
 
@@ -566,7 +559,7 @@ __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids,
     const bool self = SELF && p.mode == MODE_TOPK_SELF;
     if (self) self_score_keys<NT>(p, (uint64_t*)s_ids);
     na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
-                          s_scan, [&](int pos, int id) { s_ids[pos] = id; }, self);
+                          [&](int pos, int id) { s_ids[pos] = id; }, self);
   } else if (p.mode == MODE_LIST) {
     na = p.na;
     if (p.na_dev != nullptr) {

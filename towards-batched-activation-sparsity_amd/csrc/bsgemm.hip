@@ -372,8 +372,7 @@ __global__ __launch_bounds__(256) void bsg_score_l1_kernel(SelParams p) {
 __global__ __launch_bounds__(1024) void bsg_rank_l1_kernel(SelParams p) {
   __shared__ __attribute__((aligned(16))) uint64_t s_key[BSG_MAX_NBLK];
   __shared__ int s_rank[BSG_MAX_NBLK];
-  __shared__ int s_scan[16];
-  const int k = topk_l1_list<1024>(p.scores, p.nblk, p.k, p.bt <= 64, s_key, s_rank, s_scan,
+  const int k = topk_l1_list<1024>(p.scores, p.nblk, p.k, p.bt <= 64, s_key, s_rank,
                                   [&](int pos, int id) { p.idx_out[pos] = id; });
   if (threadIdx.x == 0) *p.na_out = k;
 }
