@@ -50,11 +50,12 @@ typedef void (*GemmFn)(GemmParams);
 enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4, KIND_VT = 5, KIND_VT1 = 6 };
 
 // 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
-// f16_self: the fp16 form compiled with the self-scored top-k (MODE_TOPK_SELF), for the 16-row
-// tiles of the MFMA kinds (null elsewhere); the other forms leave that code out.
+// f16_sel: the fp16 1-D form compiled with the in-GEMM top-k (MODE_TOPK; on 16-row tiles also
+// the self-scored MODE_TOPK_SELF), for the MFMA kinds (null for kind 3).  The other forms leave
+// that code out: carried in every kernel it cost every plain launch 0.1-0.2 us.
 struct KernelEntry {
   int kind, rows, nsub, wpg, depth;
-  GemmFn f16, bf16, f16_2d, bf16_2d, f16_self;
+  GemmFn f16, bf16, f16_2d, bf16_2d, f16_sel;
 };
 
 // A translation unit's slice of the instantiated tile set.
@@ -546,20 +547,28 @@ __device__ __forceinline__ void sort_block_list(const int32_t* ids, int na, int*
 // scores or identity) and return its length.  Ends with a barrier.  s_ids is 16-byte aligned
 // and holds BSG_MAX_NBLK ids; the top-k stages its keys in the first half and its ranks in the
 // second (up to 512 blocks).  ONE_D: the in-kernel sort of a 1-D list (p.sort_list) is compiled
-// in (the 2-D forms have none); SELF: the self-scored top-k (MODE_TOPK_SELF) is (the f16_self
-// instantiations only).
-template <int NT, bool ONE_D, bool SELF = false>
+// in (the 2-D forms have none).  SEL: the in-GEMM top-k (MODE_TOPK) is, and SELF_SCORE its
+// self-scored form (MODE_TOPK_SELF): the selection instantiations only (KernelEntry::f16_sel),
+// which alone are launched in those modes.
+template <int NT, bool ONE_D, bool SEL = false, bool SELF_SCORE = false>
 __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids, int* s_scan) {
   const int tid = threadIdx.x;
-  int na;
-  if (p.mode == MODE_TOPK || (SELF && p.mode == MODE_TOPK_SELF)) {
-    // Every work-group ranks the scores itself (identically), so the list needs no other
-    // launch; keys and ranks are staged in the list buffer and overwritten by the kept ids.
-    // MODE_TOPK_SELF computes the scores here too, so the selection needs no launch of its own.
-    const bool self = SELF && p.mode == MODE_TOPK_SELF;
-    if (self) self_score_keys<NT>(p, (uint64_t*)s_ids);
-    na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
-                          [&](int pos, int id) { s_ids[pos] = id; }, self);
+  int na = 0;
+  bool ranked = false;
+  if constexpr (SEL) {
+    if (p.mode == MODE_TOPK || (SELF_SCORE && p.mode == MODE_TOPK_SELF)) {
+      // Every work-group ranks the scores itself (identically), so the list needs no other
+      // launch; keys and ranks are staged in the list buffer and overwritten by the kept ids.
+      // MODE_TOPK_SELF computes the scores here too, so the selection needs no launch of its own.
+      const bool self = SELF_SCORE && p.mode == MODE_TOPK_SELF;
+      if (self) self_score_keys<NT>(p, (uint64_t*)s_ids);
+      na = topk_l1_list<NT>(p.scores, p.nblk, p.na, p.keyed != 0, (uint64_t*)s_ids, s_ids + BSG_MAX_NBLK / 2,
+                            [&](int pos, int id) { s_ids[pos] = id; }, self);
+      ranked = true;
+    }
+  }
+  if (ranked) {
+    // the kept list is staged
   } else if (p.mode == MODE_LIST) {
     na = p.na;
     if (p.na_dev != nullptr) {
@@ -587,8 +596,7 @@ __device__ __forceinline__ int stage_block_list(const GemmParams& p, int* s_ids,
   }
   na = __builtin_amdgcn_readfirstlane(na);
   __syncthreads();
-  if ((p.mode == MODE_TOPK || p.mode == MODE_TOPK_SELF) && p.idx_out != nullptr && blockIdx.x == 0 &&
-      blockIdx.y == 0) {
+  if (SEL && ranked && p.idx_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
     for (int i = tid; i < na; i += NT) p.idx_out[i] = s_ids[i];
     if (tid == 0) *p.na_out = na;
   }
@@ -701,7 +709,7 @@ __device__ __forceinline__ void splitk_finish(const GemmParams& p, size_t tile_l
 // the work-group's share of the block list into contiguous slices and are reduced through LDS
 // in wave order.  Each wave loads its own X fragments.  Best when bt is small (the X fragments
 // are few) and many narrow column tiles are needed to fill the chip.
-template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D, bool SELF = false>
+template <typename T, int BTT, int NSUB, int WPG, int DEPTH, bool N2D, bool SEL = false>
 __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   constexpr int NT = 64 * WPG;
   constexpr int F = BTT * NSUB;
@@ -724,7 +732,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D, SELF>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D, SEL, SEL && BTT == 1>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // This wave's contiguous slice [pbeg, pend) of the list.
@@ -805,6 +813,10 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
         compute(wv[d], xv[d]);
         BSG_TL_IF(2, u0 + d == pad);
         issue(wv[d], xv[d], u0 + d + DEPTH - pad);
+        // Keep slot d's loads between its MFMAs and slot d+1's: left free, the scheduler may
+        // gather a pass's MFMAs above its loads (each pass then waits for every block in
+        // flight: vmcnt(0)), and which kernels it does this to changes with unrelated code.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
@@ -863,7 +875,7 @@ __global__ __launch_bounds__(64 * WPG) void bsg_gemm_kernel(GemmParams p) {
 // (WK = 2): 2*WC waves, column group x 32-channel half of every block, so each wave issues half
 // the MFMAs and LDS reads of a block and two waves share each SIMD, overlapping one wave's
 // barrier and LDS waits with the other's MFMAs; the halves are summed through LDS at the end.
-template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D, bool SELF = false>
+template <typename T, int BTT, int NSUB, int WC, int WK, int DEPTH, bool N2D, bool SEL = false>
 __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p) {
   constexpr int WPG = WC * WK;
   constexpr int NT = 64 * WPG;
@@ -890,7 +902,7 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, !N2D, SELF>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, !N2D, SEL, SEL && BTT == 1>(p, s_ids, s_misc);
   BSG_TL(1);
 
   // The work-group's contiguous slice of the list (all its waves walk it together).
@@ -977,6 +989,10 @@ __global__ __launch_bounds__(64 * WC * WK) void bsg_gemm_xl_kernel(GemmParams p)
         consume(wv[d], xs[d], u0 + d);
         BSG_TL_IF(2, u0 + d == pad);
         issue(wv[d], xs[d], u0 + d + DEPTH - pad);
+        // Keep slot d's loads between its MFMAs and slot d+1's: left free, the scheduler may
+        // gather a pass's MFMAs above its loads (each pass then waits for every block in
+        // flight: vmcnt(0)), and which kernels it does this to changes with unrelated code.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
@@ -1238,7 +1254,7 @@ __device__ __forceinline__ void vt_columns(int t, int G, int T, int* first, int*
 // KH = 1 (kind 6): no channel-half split; each of the WB waves loads both halves of every
 // weight subtile and activation row tile of its blocks (the two halves of an activation row are
 // one 128-byte line, requested back to back by one wave).
-template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SELF = false>
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SEL = false>
 __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p) {
   constexpr int NW = KH * WB;
   constexpr int NT = 64 * NW;
@@ -1260,7 +1276,7 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
   BSG_TL_DECL
   BSG_TL(0);
 
-  const int na = stage_block_list<NT, true, SELF>(p, s_ids, s_misc);
+  const int na = stage_block_list<NT, true, SEL, SEL && BTT == 1>(p, s_ids, s_misc);
   BSG_TL(1);
   const int pbeg = (int)(((int64_t)na * b) / WB);
   const int pend = (int)(((int64_t)na * (b + 1)) / WB);
@@ -1301,13 +1317,17 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int hh = 0; hh < HP; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
+    // A skipped slot reads zeros through an empty resource (as its weights do), so the lanes'
+    // selects below do not depend on `ok`: a uniform branch there let the register allocator
+    // reuse an in-flight load's register and drain the pipeline (vmcnt(0)) every block.
+    const __amdgpu_buffer_rsrc_t xb = make_rsrc(p.x, ok ? p.x_bytes : 0);
     const int col = (ok ? blk : 0) * 64 + xcol;
 #pragma unroll
     for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
       for (int hh = 0; hh < HP; ++hh) {
-        const bool v = ok && xrow_ok[bi] && col + 32 * hh < p.K;
-        xd[bi][hh] = ld16(xr, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+        const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
+        xd[bi][hh] = ld16(xb, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
       }
   };
 
@@ -1333,6 +1353,10 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
         compute(wv[d], xv[d]);
         BSG_TL_IF(2, u0 + d == pad);
         issue(wv[d], xv[d], u0 + d + DEPTH - pad);
+        // Keep slot d's loads between its MFMAs and slot d+1's: left free, the scheduler may
+        // gather a pass's MFMAs above its loads (each pass then waits for every block in
+        // flight: vmcnt(0)), and which kernels it does this to changes with unrelated code.
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
@@ -1377,13 +1401,10 @@ constexpr GemmFn kernel_2d() {
   }
 }
 
-// The self-scoring fp16 form of a 16-row tile of the MFMA kinds, or null (other row counts:
-// the self-scored selection runs at most 8 rows).
+// The selection form (fp16, 1-D, in-GEMM top-k) of a tile of the MFMA kinds.
 template <int KIND, int B, int S, int W, int D>
-constexpr GemmFn kernel_self() {
-  if constexpr (B != 1) {
-    return nullptr;
-  } else if constexpr (KIND == KIND_KSPLIT) {
+constexpr GemmFn kernel_sel() {
+  if constexpr (KIND == KIND_KSPLIT) {
     return bsg_gemm_kernel<_Float16, B, S, W, D, false, true>;
   } else if constexpr (KIND == KIND_XLDS) {
     return bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false, true>;
@@ -1399,21 +1420,21 @@ constexpr GemmFn kernel_self() {
 #define BSG_K(B, S, W, D)                                                                                          \
   {KIND_KSPLIT, 16 * B, S, W, D, bsg_gemm_kernel<_Float16, B, S, W, D, false>, bsg_gemm_kernel<__bf16, B, S, W, D, false>, \
    kernel_2d<KIND_KSPLIT, _Float16, B, S, W, D>(), kernel_2d<KIND_KSPLIT, __bf16, B, S, W, D>(),                   \
-   kernel_self<KIND_KSPLIT, B, S, W, D>()}
+   kernel_sel<KIND_KSPLIT, B, S, W, D>()}
 #define BSG_X(B, S, W, D)                                                                     \
   {KIND_XLDS, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W, 1, D, false>,           \
    bsg_gemm_xl_kernel<__bf16, B, S, W, 1, D, false>, kernel_2d<KIND_XLDS, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>(), kernel_self<KIND_XLDS, B, S, W, D>()}
+   kernel_2d<KIND_XLDS, __bf16, B, S, W, D>(), kernel_sel<KIND_XLDS, B, S, W, D>()}
 #define BSG_Y(B, S, W, D)                                                                        \
   {KIND_XLDS_KH, 16 * B, S, W, D, bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false>,        \
    bsg_gemm_xl_kernel<__bf16, B, S, W / 2, 2, D, false>, kernel_2d<KIND_XLDS_KH, _Float16, B, S, W, D>(), \
-   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>(), kernel_self<KIND_XLDS_KH, B, S, W, D>()}
+   kernel_2d<KIND_XLDS_KH, __bf16, B, S, W, D>(), kernel_sel<KIND_XLDS_KH, B, S, W, D>()}
 #define BSG_V(B, S, W, D)                                                                               \
   {KIND_VT, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W / 2, D>, bsg_gemm_vt_kernel<__bf16, B, S, W / 2, D>, \
-   nullptr, nullptr, kernel_self<KIND_VT, B, S, W, D>()}
+   nullptr, nullptr, kernel_sel<KIND_VT, B, S, W, D>()}
 #define BSG_V1(B, S, W, D)                                                                                \
   {KIND_VT1, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1>, bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1>, \
-   nullptr, nullptr, kernel_self<KIND_VT1, B, S, W, D>()}
+   nullptr, nullptr, kernel_sel<KIND_VT1, B, S, W, D>()}
 #define BSG_F(R, S, W, D)                                                                                 \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
    kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>(), nullptr}

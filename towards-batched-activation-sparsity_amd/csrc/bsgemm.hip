@@ -811,11 +811,13 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
 
   dim3 grid((unsigned)(n_tiles * pl.split_k), (unsigned)ygroups, 1);
   dim3 block((unsigned)(64 * pl.waves_per_group), 1, 1);
-  GemmFn fn = mode == MODE_TOPK_SELF ? ke->f16_self
+  const bool topk = mode == MODE_TOPK || mode == MODE_TOPK_SELF;
+  GemmFn fn = topk ? (dtype == BSG_F16 ? ke->f16_sel : nullptr)
               : ex.nidx != nullptr ? (dtype == BSG_F16 ? ke->f16_2d : ke->bf16_2d)
                                    : (dtype == BSG_F16 ? ke->f16 : ke->bf16);
-  if (fn == nullptr && mode == MODE_TOPK_SELF)
-    return fail(BSG_ERR_UNSUPPORTED, "self-scored top-k: no instantiation for this tile (16-row MFMA tiles only)");
+  if (topk && (fn == nullptr || (mode == MODE_TOPK_SELF && pl.rows_per_group != 16)))
+    return fail(BSG_ERR_UNSUPPORTED, "top-k in the GEMM: no selection instantiation for this tile (fp16, MFMA kinds; "
+                "self-scored: 16-row tiles)");
   if (fn == nullptr) return fail(BSG_ERR_UNSUPPORTED, "2-D: no instantiation for this tile");
   // Kind 3: LDS for the staged activations of the whole list (na is the list capacity; a
   // device-side count or a bitmap only shortens it).
@@ -1179,11 +1181,11 @@ static int select_gemm_run(const void* x, int64_t ldx, int64_t bt, int64_t K, in
   // the rank launch that 8 forced).  Otherwise a
   // one-work-group rank launch (about 3 us) is cheaper than ranking in each work-group.
   const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
-  const bool rank_in_gemm =
-      nblk <= BSG_TOPK_MAX_NBLK && items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group;
   const KernelEntry* ke = find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
-  if (rank_in_gemm && bt <= BSG_SELF_MAX_ROWS && bt * K * 2 <= BSG_SELF_SCORE_MAX_X_BYTES && ke != nullptr &&
-      ke->f16_self != nullptr) {
+  const bool rank_in_gemm = nblk <= BSG_TOPK_MAX_NBLK && ke != nullptr && ke->f16_sel != nullptr &&
+                            items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group;
+  if (rank_in_gemm && bt <= BSG_SELF_MAX_ROWS && bt * K * 2 <= BSG_SELF_SCORE_MAX_X_BYTES &&
+      pl.rows_per_group == 16) {
     // One launch: every GEMM work-group scores the blocks from x itself, ranks them and walks
     // the kept list; no score buffer is written.
     rc = select_l1_check(x, ldx, bt, K, k, idx_out, na_out, dtype);
