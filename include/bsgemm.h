@@ -226,8 +226,8 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
 
 /* Selector followed by the GEMM on its device-side list, both on `stream`; idx_out and
  * *na_out receive the kept list and count as from bsg_select_topk_l1.  Where the plan's waves
- * can rank the scores quickly (nblk <= 512 and at most 12 items of 64 blocks x 16 scores per
- * wave) every GEMM work-group ranks them itself and the call is two launches (scores, GEMM);
+ * can rank the scores quickly (an MFMA kind, nblk <= 512 and at most 12 items of 64 blocks x 16
+ * scores per wave) every GEMM work-group ranks them itself and the call is two launches (scores, GEMM);
  * at small batches (bt <= 8 and bt x K x 2 <= 24 KiB, MFMA kinds) every GEMM work-group also
  * computes the scores from x itself and the call is one launch; otherwise three (scores,
  * top-k, GEMM).  The selection is the same in every form.  ws is split: the first bsg_select_workspace_bytes(K)

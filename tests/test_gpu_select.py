@@ -95,7 +95,7 @@ def _fused(dev, x, w_nk, k, plan=None):
     (64, 11008, 4096, 83, (4, 16, 4, 4, 64, 2)),  # 172 blocks over 4 waves (9 rank items each); in the GEMM
     (16, 4096, 4096, 23, (1, 16, 1, 4, 16, 1)),   # one wave ranks 64 blocks; in the GEMM
     (16, 11008, 4096, 86, (1, 16, 2, 4, 16, 1)),  # 172 blocks, 2 waves: rank launch, then the list
-    (2, 4096, 4096, 13, (1, 16, 4, 4, 2, 3)),     # dot-product kernel; in the GEMM
+    (2, 4096, 4096, 13, (1, 16, 4, 4, 2, 3)),     # dot-product kernel: rank launch, then the list
     (80, 4096, 1024, 20, None),                   # > 64 rows: pair compares, two grid rows
     (8, 32768, 256, 100, (1, 16, 1, 4, 16, 1)),   # 512 blocks: rank launch
     (4, 38400, 256, 77, None),                    # 600 blocks: rank launch
