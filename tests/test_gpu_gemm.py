@@ -393,6 +393,24 @@ def test_in_kernel_sort_matches_sort_then_gemm(dev, plan):
     assert_close(got.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.sort(ids[:12])), "device count")
 
 
+def test_in_kernel_sort_bf16(dev):
+    """The in-kernel sort is dtype-blind: bf16 inputs give, bit for bit, the GEMM on the sorted list."""
+    bt, k, n = 16, 4096, 512
+    x, w_nk, _ = case(26, bt, k, n, 1)
+    xb = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).to(dev)
+    packed = bsa.pack_weight(torch.from_numpy(w_nk.astype(np.float32)).to(torch.bfloat16).to(dev))
+    ids = SORT_LISTS["random"].astype(np.int32)
+    for plan in ((1, 16, 2, 4, 16, 1), (1, 16, 4, 4, 16, 6)):
+        got = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
+        want = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
+        bsa.gemm_packed(xb, packed, n, to_dev(ids, dev), got, plan=bsa.Plan(*plan), workspace_prefix="isort_bf",
+                        sort_list=True)
+        bsa.gemm_packed(xb, packed, n, to_dev(np.sort(ids), dev), want, plan=bsa.Plan(*plan),
+                        workspace_prefix="isort_bf_ref")
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"bf16 in-kernel sort, plan {plan}"
+
+
 def test_in_kernel_sort_at_its_limit_and_past_it(dev):
     """1024 entries (MAX_NBLK // 2, the in-kernel sort's limit) sorted in the GEMM; the drop-in
     sorts a longer list with a sort launch first (same result)."""
