@@ -26,13 +26,15 @@ cpu_baseline = the oracle's CPU path (torch CPU gather + fp32 matmul, every host
 The same line also carries, measured in the same run after the matrix (skip with --no-extras):
 fused_select_gemm = configs[3] (exact-L1 select k=31 of 64 + gate/up GEMM at B=64, indices
 checked bit-exact), fused_select_gemm_b2 = the same call at q/k/v/o B=2 k=32 (one launch: the
-GEMM scores the blocks itself), decode_step = configs[4] (the 32-layer decode step of linears as one
+GEMM scores the blocks itself), rule_select_gemm = the reference's decode linear with its own
+selection rule (L2 mean, RRD:179-284) as one library call, beside its torch selection and in eager
+calls of the model patch, decode_step = configs[4] (the 32-layer decode step of linears as one
 hipGraph), eager_calls = the host cost of one eager call of the drop-in entry points (what
 the model patch pays per linear layer), perstep_replay = the reference's headline table (its
 per-step sparsity maps of the 224-GEMM decode step) at B=2, 4, 8, 16, 32, 64.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload llama|down_sweep|fused|decode|perstep|2d] [--only POINT]
+                    [--workload llama|down_sweep|fused|rule|decode|perstep|2d] [--only POINT]
 """
 from __future__ import annotations
 
@@ -83,7 +85,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="llama",
-                    choices=["llama", "down_sweep", "fused", "decode", "perstep", "2d", "timeline"])
+                    choices=["llama", "down_sweep", "fused", "rule", "decode", "perstep", "2d", "timeline"])
     ap.add_argument("--plan", default=None,
                     help="timeline workload, or llama/down_sweep with --only: explicit plan a,b,c,d,e,f "
                          "(default: tuned)")
@@ -167,6 +169,7 @@ class Point:
         self.flops = 2 * bt * self.na * 64 * self.n
         self.copies = min(pool.copies, copies_for(self.active_bytes))
         self.graph = None
+        self.in_step = True  # part of the timed step graph (comparison points are timed alone)
 
     @property
     def replay_bytes(self) -> int:
@@ -456,9 +459,15 @@ def sname(s: float) -> str:
     return f"s{int(round(s * 1000)):03d}"
 
 
+# Suffix of the comparison points that run a B=2 sparse point on the dot-product kernel (kind 3,
+# fp32 dot products with DPP quad sums) instead of the table's MFMA plan.
+FMA_SUFFIX = "_fma"
+
+
 def matrix_points(workload, dev):
     """The points of the llama (configs[2] + the configs[1] sweep) or down_sweep workload:
-    [(name, shape, B, na, dense)]."""
+    [(name, shape, B, na, dense)].  The llama workload also holds, for each B=2 sparse point, a
+    twin named <point>_fma on the dot-product kernel (timed on its own graph, outside the step)."""
     from oracle import bsg_oracle as orc
 
     rows = []
@@ -475,6 +484,8 @@ def matrix_points(workload, dev):
         name = "down_b16_dense" if s == 0.0 else f"down_b16_{sname(s)}"
         if name not in have:
             rows.append((name, "down", 16, nb if s == 0.0 else orc.n_active_for_sparsity(s, nb), s == 0.0))
+    if workload == "llama":
+        rows += [(r[0] + FMA_SUFFIX,) + r[1:] for r in list(rows) if r[2] == 2 and not r[4]]
     return rows
 
 
@@ -485,6 +496,29 @@ def pool_copies(rows):
     for _, sh, _, na, _ in rows:
         need[sh] = max(need.get(sh, 1), copies_for(na * 64 * SHAPES[sh][1] * 2))
     return need
+
+
+def best_fma_plan(pool, bt, na, dev, inputs, reps=3):
+    """The fastest dot-product (kind 3) plan for a point, each candidate the tuner would try
+    (every instantiated kind-3 tile for the batch) timed on the point's own rotated graph."""
+    import bsa_mi355x as bsa
+    from bsa_mi355x import tuning
+
+    best = None
+    for cand in tuning.candidate_plans(bt, na, pool.nblk):
+        if cand.kind != 3:
+            continue
+        try:
+            pt = Point("fma_probe", pool, bt, na, dev, plan=cand, inputs=inputs)
+        except (RuntimeError, ValueError):
+            continue  # a tile whose activation staging cannot hold this list
+        if pt.plan.kind != 3:
+            continue
+        med, _ = _graph_time([lambda i=i: pt.launch(i) for i in range(pt.copies)], reps)
+        us = med / pt.copies
+        if best is None or us < best[0]:
+            best = (us, bsa.Plan(*pt.plan.as_tuple()))
+    return None if best is None else best[1]
 
 
 def run_matrix(args, dev):
@@ -517,7 +551,14 @@ def run_matrix(args, dev):
     points = []
     for name, sh, bt, na, dense in rows:
         x, masks = drawn[(sh, bt)]
-        points.append(Point(name, pools[sh], bt, na, dev, dense=dense, plan=forced, inputs=(x, masks[na])))
+        plan = forced
+        if name.endswith(FMA_SUFFIX) and forced is None:
+            plan = best_fma_plan(pools[sh], bt, na, dev, (x, masks[na]))
+            if plan is None:
+                log(f"{name}: no dot-product tile runs this point; skipped")
+                continue
+        points.append(Point(name, pools[sh], bt, na, dev, dense=dense, plan=plan, inputs=(x, masks[na])))
+        points[-1].in_step = not name.endswith(FMA_SUFFIX)
         log(f"prepared {name}: na={points[-1].na} copies={points[-1].copies} "
             f"replay={points[-1].replay_bytes / 2**30:.2f} GiB plan={points[-1].plan}")
     bad = []
@@ -530,11 +571,12 @@ def run_matrix(args, dev):
     log("parity ok on every point")
     for p in points:
         p.capture()
-    step_graph = capture_step(points)
+    step_points = [p for p in points if p.in_step]
+    step_graph = capture_step(step_points)
     log("graphs captured")
 
     total_ms, wall, per = time_points(points, step_graph, args.steps, args.warmup)
-    step_bytes = sum(p.replay_bytes for p in points)
+    step_bytes = sum(p.replay_bytes for p in step_points)
     value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
     log(f"timed {args.steps} steps in {total_ms:.2f} ms (host wall {wall * 1e3:.1f} ms)")
 
@@ -557,11 +599,22 @@ def run_matrix(args, dev):
                 row["speedup_vs_dense"] = round(d / med, 3)
                 row["ideal_speedup"] = round(p.nblk / p.na, 3)
                 row["speedup_over_ideal"] = round((d / med) / (p.nblk / p.na), 3)
+        if p.name.endswith(FMA_SUFFIX):
+            twin = p.name[: -len(FMA_SUFFIX)]
+            row["in_step"] = False
+            row["mfma_point"] = twin
+            row["mfma_us_per_gemm"] = round(per[twin][0], 3)
+            row["fma_over_mfma_time"] = round(med / per[twin][0], 3)
+        if not args.only:
+            # the practical read of the same bytes per launch (same rotation and timing)
+            rd = read_calibration_us(p)
+            row["practical_read_us"] = round(rd, 3)
+            row["frac_of_practical_read"] = round(rd / med, 4)
         out_points.append(row)
         log(json.dumps(row))
 
-    shares = kernel_shares(points, per)
-    focus = roofline_point(points, shares) if not args.only else points[0].name
+    shares = kernel_shares(step_points, per)
+    focus = roofline_point(step_points, shares) if not args.only else points[0].name
 
     def roofline_of(name, with_read):
         fp = next(p for p in points if p.name == name)
@@ -615,6 +668,11 @@ def run_matrix(args, dev):
         extras["fused_select_gemm_b2"] = measure_fused(args, dev, shape="qkvo", bt=2, keep=32)
         log(f"select + GEMM at q/k/v/o B=2: {extras['fused_select_gemm_b2']['us_select_plus_gemm']} us "
             f"(GEMM alone {extras['fused_select_gemm_b2']['us_gemm_only']} us)")
+        log("the reference's decode linear (its selection rule) as one call ...")
+        extras["rule_select_gemm"] = measure_rule_linear(args, dev)
+        log(f"reference-rule select + GEMM: {extras['rule_select_gemm']['us_fused_rule_select_gemm']} us fused, "
+            f"{extras['rule_select_gemm']['us_reference_torch_select_then_gemm']} us with the reference's torch "
+            f"selection (GEMM alone {extras['rule_select_gemm']['us_gemm_only']} us)")
         log("configs[4]: 32-layer decode step ...")
         extras["decode_step"] = measure_decode(args, dev)
         log(f"configs[4] done ({time.perf_counter() - t0:.1f} s): {extras['decode_step']['ms_per_step']} ms/step")
@@ -642,7 +700,8 @@ def run_matrix(args, dev):
         for p, row in zip(points, out_points):
             row["cpu_us_per_gemm"] = round(cpu_point_us(p), 1)
             row["gpu_speedup_over_cpu"] = round(row["cpu_us_per_gemm"] / row["us_per_gemm"], 1)
-    sparse = [r for r in out_points if "speedup_over_ideal" in r]
+    sparse = [r for r in out_points if "speedup_over_ideal" in r and r.get("in_step", True)]
+    fma_rows = [r for r in out_points if not r.get("in_step", True)]
     if args.workload == "llama":
         workload = ("Llama-2-7B q/k/v/o (4096->4096), gate/up (4096->11008), down (11008->4096) at B=2@0.803, "
                     "B=16@0.638, B=64@0.520, each with its dense point (configs[2]); plus the down_proj B=16 "
@@ -664,14 +723,22 @@ def run_matrix(args, dev):
         "data": "synthetic: numpy PCG64 seed 1234, W~N(0,0.02) stored [K,N], X~Laplace(0,0.05) (down) / N(0,1) "
                 "(others), masks rng.choice sorted; each point's graph rotates over >=1 GiB of distinct active "
                 "weight",
-        "config": {"workload": workload, "gemms_per_step": sum(p.copies for p in points),
-                   "value_is": "active-weight bytes / timed seconds over all points",
+        "config": {"workload": workload, "gemms_per_step": sum(p.copies for p in step_points),
+                   "value_is": "active-weight bytes / timed seconds over all points of the step (the "
+                               "dot-product comparison points are timed on their own graphs, outside it)",
                    "min_replay_GiB": round(min(p.replay_bytes for p in points) / 2**30, 3)},
         "points": out_points,
         "summary": {
             "sparse_points": len(sparse),
             "mean_frac_hbm_peak_sparse": round(statistics.mean(r["frac_hbm_peak"] for r in sparse), 4) if sparse else None,
             "mean_speedup_over_ideal": round(statistics.mean(r["speedup_over_ideal"] for r in sparse), 4) if sparse else None,
+            "mean_frac_of_practical_read": round(statistics.mean(r["frac_of_practical_read"] for r in out_points
+                                                                 if "frac_of_practical_read" in r), 4)
+            if any("frac_of_practical_read" in r for r in out_points) else None,
+            "b64_frac_of_practical_read": {r["name"]: r["frac_of_practical_read"] for r in out_points
+                                           if r["B"] == 64 and "frac_of_practical_read" in r},
+            "dot_product_vs_mfma_at_b2": {r["mfma_point"]: {"fma_us": r["us_per_gemm"], "mfma_us": r["mfma_us_per_gemm"],
+                                                             "fma_plan": r["plan"]} for r in fma_rows},
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -820,9 +887,19 @@ def measure_eager(args, dev):
     y_ref = orc.gemm_ref(x2d.float().cpu().numpy(), w.float().cpu().numpy(), ids_sorted.cpu().numpy())
     if not orc.within_tolerance(y2d.float().cpu().numpy(), y_ref):
         raise SystemExit("eager drop-in output outside tolerance")
+    # fresh activation and output tensors per call (a decode loop's x and out are new each token)
+    xs = [x.clone() for _ in range(4)]
+    outs = [torch.empty_like(out) for _ in range(4)]
+    turn = [0]
+
+    def dropin_fresh():
+        i = turn[0] = (turn[0] + 1) & 3
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(xs[i], w, ids, outs[i], cache_prefix="eager_bench")
+
     calls = {
         "dropin_unsorted_list": lambda: bsa._prepacked_block_sparse_gemm_from_active_blocks(
             x, w, ids, out, cache_prefix="eager_bench"),
+        "dropin_fresh_x_and_out": dropin_fresh,
         "gemm_packed_table_plan": lambda: bsa.gemm_packed(x2d, packed, n, ids_sorted, y2d,
                                                           workspace_prefix="eager_bench_packed"),
         "select_gemm_packed": lambda: select_gemm_packed(x2d, packed, n, na, y2d, idx_out=idx, count_out=cnt,
@@ -911,6 +988,114 @@ def measure_fused(args, dev, shape="gate_up", bt=64, keep=31):
            "plan": list(plan.as_tuple()), "plan_gemm_only": list(plan_gemm.as_tuple()), "launches_per_replay": r, "replays": reps, "indices_bit_exact": True,
            **cpu}
     del pool, pt
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_rule_linear(args, dev, shape="gate_up", bt=64, density=0.48):
+    """The reference's decode linear (`_sparse_linear`, RRD:179-284) on gate/up at B=64: its own
+    selection rule (`_select_active_blocks`: batch-mean L2 norm, n_keep = round(0.48 x 64) = 31)
+    then the GEMM.  Timed as graphs rotated over >= 1 GiB of active weight, three ways: one
+    library call (bsg_select_gemm_rule: score launch + a GEMM that ranks the scores itself),
+    the library's selector then the GEMM on its device count (three launches), and the
+    reference's torch selection (norm, mean, topk, sort: its op chain, RRD:97-113) then the GEMM.
+    Then eager calls of the model patch's `_sparse_linear` (what a decode step pays per linear),
+    fused and with selection and GEMM as separate calls.  Ids are checked against the oracle
+    (float64, select_scored_ref) first."""
+    import numpy as np
+    import torch
+
+    import bsa_mi355x as bsa
+    from bsa_mi355x import patch
+    from bsa_mi355x.select import select_gemm_rule_packed
+    from oracle import bsg_oracle as orc
+
+    k, n = SHAPES[shape]
+    nblk = k // 64
+    keep = orc.n_keep(density, nblk)
+    pool = ShapePool(shape, k, n, dev, copies_for(keep * 64 * n * 2))
+    pt = Point(f"{shape}_b{bt}_rule", pool, bt, keep, dev)
+    idx = torch.empty(keep, dtype=torch.int32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    select_gemm_rule_packed(pt.x, pool.packed[0], n, keep, pt.y, score="l2_mean", idx_out=idx, count_out=cnt,
+                            workspace_prefix="rule_bench")
+    torch.cuda.synchronize()
+    want, _, _ = orc.select_scored_ref(pt.x_np, keep, "l2_mean")
+    if not np.array_equal(idx.cpu().numpy(), want) or int(cnt.item()) != keep:
+        raise SystemExit("reference-rule selection differs from the oracle")
+    if not orc.within_tolerance(pt.y.float().cpu().numpy(),
+                                orc.gemm_ref(pt.x_np, np.ascontiguousarray(pool.w_kn_np.T), want)):
+        raise SystemExit("reference-rule select + GEMM output outside tolerance")
+    plan = bsa.resolve_plan(bt, n, nblk, keep, dev, select=True)
+    plan_gemm = bsa.resolve_plan(bt, n, nblk, keep, dev)
+    x3 = pt.x.view(bt, 1, k)
+
+    def fused(i):
+        return lambda: select_gemm_rule_packed(pt.x, pool.packed[i], n, keep, pt.y, score="l2_mean", plan=plan,
+                                               idx_out=idx, count_out=cnt, workspace_prefix="rule_bench")
+
+    def separate(i):
+        def f():
+            bsa.select_topk(pt.x, keep, score="l2_mean", idx_out=idx, count_out=cnt, workspace_prefix="rule_sel")
+            bsa.gemm_packed(pt.x, pool.packed[i], n, idx, pt.y, num_active=keep, num_active_dev=cnt, plan=plan_gemm,
+                            workspace_prefix="rule_gemm")
+        return f
+
+    def torch_select(i):
+        def f():
+            xb = x3[..., : nblk * 64].float().reshape(-1, nblk, 64)
+            sel = torch.topk(xb.norm(dim=2).mean(dim=0), k=keep).indices.sort()[0].to(torch.int32)
+            bsa.gemm_packed(pt.x, pool.packed[i], n, sel, pt.y, num_active=keep, plan=plan_gemm,
+                            workspace_prefix="rule_gemm_t")
+        return f
+
+    def gemm_only(i):
+        return lambda: bsa.gemm_packed(pt.x, pool.packed[i], n, idx, pt.y, num_active=keep, plan=plan_gemm,
+                                       workspace_prefix="rule_gemm")
+
+    r = pt.copies
+    reps = max(5, args.steps)
+    t = {name: _graph_time([fn(i) for i in range(r)], reps)[0] / r
+         for name, fn in (("fused", fused), ("separate", separate), ("torch_select", torch_select),
+                          ("gemm_only", gemm_only))}
+    # eager: the patched linear per call (a decode step calls it once per projection)
+    w = torch.from_numpy(np.ascontiguousarray(pool.w_kn_np.T)).to(dev)
+    cfg = {"best_kern": "naive", "best_K": 1, "best_tile": None}
+    stats = {"calls": 0, "wall_s": 0.0}
+
+    def eager_fused():
+        patch._sparse_linear(x3, w, density, cfg, "rule_eager", 64, stats, False, None)
+
+    def eager_separate():
+        sel = bsa._select_active_blocks(x3, density, 64)
+        out = torch.empty(bt, 1, n, dtype=torch.float16, device=dev)
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(x3, w, sel, out, cache_prefix="rule_eager",
+                                                            use_run_compressed=False)
+
+    eager = {}
+    for name, fn in (("patched_linear_fused", eager_fused), ("select_then_gemm_calls", eager_separate)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        n_calls = 500
+        t0 = time.perf_counter()
+        for _ in range(n_calls):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        eager[name] = {"host_us": round((t1 - t0) / n_calls * 1e6, 2), "wall_us": round((t2 - t0) / n_calls * 1e6, 2)}
+    out = {"workload": f"the reference's decode linear (L2-mean rule, k={keep} of {nblk}) + sparse GEMM, {shape} "
+                       f"B={bt} K={k} N={n}: RRD:179-284 with _select_active_blocks",
+           "us_fused_rule_select_gemm": round(t["fused"], 3),
+           "us_library_select_then_gemm": round(t["separate"], 3),
+           "us_reference_torch_select_then_gemm": round(t["torch_select"], 3),
+           "us_gemm_only": round(t["gemm_only"], 3),
+           "select_overhead_us_fused": round(t["fused"] - t["gemm_only"], 3),
+           "select_overhead_us_reference_torch": round(t["torch_select"] - t["gemm_only"], 3),
+           "plan": list(plan.as_tuple()), "plan_gemm_only": list(plan_gemm.as_tuple()), "indices_bit_exact": True,
+           "eager": eager, "launches_per_replay": r, "replays": reps}
+    del pool, pt, w
     torch.cuda.empty_cache()
     return out
 
@@ -1380,6 +1565,8 @@ def main():
         run_matrix(args, dev)
     elif args.workload == "fused":
         run_fused(args, dev)
+    elif args.workload == "rule":
+        print(json.dumps({"metric": METRIC, "rule_select_gemm": measure_rule_linear(args, dev)}), flush=True)
     elif args.workload == "perstep":
         run_perstep(args, dev)
     elif args.workload == "2d":

@@ -50,19 +50,39 @@ enum bsg_status {
 /* Launch plan of the GEMM.  A zero field means "choose automatically".
  *   split_k         : work-groups that share one output tile and split the active-block
  *                     list (fp32 partials + in-kernel deterministic reduction), >= 1
- *   cols_per_wave   : output columns per wavefront: 16, 32, 64 or 128
+ *   cols_per_wave   : output columns per wavefront (kinds 1-4: 16, 32, 64 or 128); kinds 5
+ *                     and 6: the most columns one work-group may take (16 x its most subtiles)
  *   waves_per_group : wavefronts per work-group: 1, 2, 4 or 8
  *   depth           : K-blocks whose loads each wave keeps in flight: 1, 2, 4 or 8
  *   rows_per_group  : batch rows per work-group (16, 32 or 64; 1, 2, 4 or 8 for kind 3); bt
  *                     above it adds grid rows
- *   kind            : 1 = the waves of a work-group split its block list (each loads its own
- *                     activation fragments); 2 = the waves split the work-group's columns and
- *                     share each block's activation tile through LDS (work-group columns =
- *                     cols_per_wave * waves_per_group); 3 = fp32 dot products instead of MFMA
- *                     for 1-8 rows, the work-group's activations staged in LDS once, split_k 1,
- *                     only when named (automatic plans take kinds 1-2); 4 = as 2, with the waves
- *                     split over columns and over the two 32-channel halves of every block (two
- *                     waves per SIMD; work-group columns = cols_per_wave * waves_per_group / 2)
+ *   kind            : the kernel family.
+ *     1  the waves of a work-group split its block list, each loading its own activation
+ *        fragments; work-group columns = cols_per_wave.  Any split_k.
+ *     2  the waves split the work-group's columns and share each block's activation tile
+ *        through LDS; work-group columns = cols_per_wave * waves_per_group.  Any split_k.
+ *     3  fp32 dot products instead of MFMA, for 1-8 rows; each wave stages the activations of
+ *        its slice of the list in LDS once and the quads of lanes meet through DPP; work-group
+ *        columns = cols_per_wave; split_k must be 1; runs only when a plan names it.
+ *     4  as 2, with the waves split over columns and over the two 32-channel halves of every
+ *        block (two waves per SIMD); work-group columns = cols_per_wave * waves_per_group / 2;
+ *        waves_per_group 4 or 8.  Any split_k.
+ *     5  variable-width column groups: the ceil(N/16) 16-column subtiles are dealt as evenly as
+ *        possible over G = min(ceil(N/16), max(CUs / row groups, ceil(N / cols_per_wave)))
+ *        work-groups per row group, so a group takes at most cols_per_wave columns and any N
+ *        fills every compute unit without split-K.  Waves = 32-channel half x block slice
+ *        (waves_per_group even: waves_per_group / 2 slices of the list); every weight and
+ *        activation byte of a group is loaded by one wave, straight into registers, and the
+ *        waves meet in LDS once at the end.  split_k must be 1 (0 resolves to 1).
+ *     6  as 5, with the waves splitting the block list only (waves_per_group slices), each
+ *        loading both channel halves of its blocks.  split_k must be 1.
+ *   Kinds 5 and 6 run 1-D lists only (bsg_gemm_2d rejects them), and only the tiles compiled
+ *   into the library resolve (BSG_ERR_UNSUPPORTED names any other); a zero field of a kind 5/6
+ *   plan takes rows 16/32/64 from bt, cols_per_wave 48, waves_per_group 4, depth 4.
+ * kind 0 here resolves by heuristic to kind 1 (bt <= 16) or kind 2 (larger bt).  The Python
+ * layer does not rely on it: its plans come from a table tuned on the MI355X
+ * (bsa_mi355x/tuned_plans.json) whose entries name kinds 1, 2, 4, 5 and 6, or from first-call
+ * tuning of problems the table does not hold.
  * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
  * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
 typedef struct bsg_plan {
@@ -124,7 +144,10 @@ int bsg_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K,
 
 /* bsg_gemm with the list sorted ascending inside the GEMM's own list staging (no separate sort
  * launch): the same arguments, the same result as an ascending sort of the list followed by
- * bsg_gemm, bit for bit.  num_active <= BSG_MAX_NBLK / 2 (else BSG_ERR_UNSUPPORTED).
+ * bsg_gemm, bit for bit.  With num_active_dev the count is applied first: only the first
+ * min(*num_active_dev, num_active) entries are sorted and used, so the result is bsg_gemm on
+ * sort(active_blocks[0 .. count)), not on the count smallest ids of the whole list.
+ * num_active <= BSG_MAX_NBLK / 2 (else BSG_ERR_UNSUPPORTED).
  * Replaces the sort + GEMM pair of _prepacked_block_sparse_gemm_from_active_blocks with
  * sort_active_blocks=True: _sort_active_blocks_asc (…min_runtime.py:140-163, called at
  * :3193-3194) followed by prepacked_block_sparse_gemm_batched_kernel (…min_runtime.py:684-733). */
@@ -207,8 +230,9 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
  *                   energy (unscaled, in score order) reaches energy_keep of the total; idx_out
  *                   then needs room for floor(K/64) entries                     (RRD:155-176)
  *   ratio_out     : kept energy fraction (float, device), as RRD:141 / RRD:176 return it
- * Ranking is (score desc, block id asc); idx_out holds the kept ids ascending and *na_out
- * their count, both on the device.  Workspace as bsg_select_topk_l1.  Replaces
+ * Ranking is (score desc, block id asc), on the fp64 scores: -0 ties with +0, and a NaN score
+ * ranks above every number (as torch.topk ranks NaN).  idx_out holds the kept ids ascending and
+ * *na_out their count, both on the device.  Workspace as bsg_select_topk_l1.  Replaces
  * _select_active_blocks (RRD:90-113), _topk_energy_ratio (RRD:116-141) and
  * _energy_expanded_active_blocks (RRD:144-176). */
 enum bsg_score { BSG_SCORE_L1 = 0, BSG_SCORE_L2_MEAN = 1, BSG_SCORE_ENERGY = 2 };
@@ -239,6 +263,22 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
                     void* y, int64_t ldy, int dtype,
                     void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
 
+/* Selection by the reference's own rules (bsg_select_opts, as bsg_select_topk) followed by the
+ * GEMM on the kept blocks, both on `stream`, with no host round trip: the decode linear of
+ * _sparse_linear (scripts/bench_roundrobin_e2e_decode.py:179-284), whose selection is
+ * _select_active_blocks (RRD:90-113), or _energy_expanded_active_blocks (RRD:144-176) with an
+ * energy budget.  idx_out, *na_out and ratio_out receive exactly what bsg_select_topk gives for
+ * the same x and opts (idx_out needs room for floor(K/64) ids under an energy budget, min(k,
+ * floor(K/64)) otherwise).  Two launches (fp64 order keys of the block scores, then the GEMM,
+ * whose work-groups rank the keys themselves) when there is no energy budget, no ratio_out, the
+ * dtype is fp16 and the plan's waves can rank the blocks (as bsg_select_gemm); otherwise three
+ * (scores, one-work-group rank, GEMM on the device count).  opts->score == BSG_SCORE_L1 is
+ * bsg_select_gemm.  Workspace as bsg_select_gemm: bsg_select_workspace_bytes(K) bytes for the
+ * selector, then the GEMM's. */
+int bsg_select_gemm_rule(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
+                         const void* wp, int64_t N, int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy,
+                         int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream);
+
 /* Allocation-free variant of bsg_select_gemm.  It has no counterpart in the reference: it is for
  * callers that cannot allocate or hand over device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  Same arguments, selection, kernels and results
@@ -247,7 +287,9 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
  * BSG_NOALLOC_SCRATCH_BYTES on each GPU it runs on (held until the process ends).  Layout: 64 KiB
  * of tile arrival counters, 16 KiB of block scores, the rest for partials.  A call whose plan
  * needs more partials or counters than that returns BSG_ERR_WORKSPACE before any launch.  The
- * first call on a device looks the array up and clears its counters (a kernel on `stream`).
+ * first call on a device looks the array up and clears its counters (a kernel on `stream`; when
+ * that first call is made under stream capture, the lookup runs in the relaxed capture mode and
+ * the clear is recorded into the graph, so it runs at the start of every replay).
  * Nothing is allocated and no allocating library routine is called.  Every call on one GPU shares
  * that GPU's array, so calls that overlap on one GPU (concurrent streams, or host threads) race
  * and must be serialised by the caller. */

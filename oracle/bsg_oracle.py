@@ -28,6 +28,8 @@ How each function is pinned (tests/test_oracle.py):
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 BLOCK_K = 64  # KRN:17 INDEX_BLOCK_META_SIZE
@@ -244,6 +246,7 @@ def select_scored_ref(x: np.ndarray, k: int, score: str = "l2_mean", prior=None,
       keep   = min(k, nblk), grown while energy_keep > 0 and the top-keep energy share is below
                it, to searchsorted(cum, energy_keep * total) + 1 clamped to [k, nblk] (RRD:165-176);
       ratio  = cumulative energy at keep / max(total, 1e-12) (RRD:141, 176).
+    A NaN score ranks above every number (torch.topk's order for NaN) and -0 ties with +0.
     Returns (ids ascending int32, keep, ratio)."""
     l2, energy, es = block_stats64(x, scale)
     nb = len(energy)
@@ -251,7 +254,7 @@ def select_scored_ref(x: np.ndarray, k: int, score: str = "l2_mean", prior=None,
     if prior is not None and np.asarray(prior).size == nb:  # any other length is ignored (RRD:110-112)
         pr = np.asarray(prior, dtype=np.float64).reshape(-1) + float(eps)
         sc = sc * np.maximum(pr, 1e-6) ** float(alpha)
-    order = sorted(range(nb), key=lambda j: (-float(sc[j]), j))
+    order = sorted(range(nb), key=lambda j: (-math.inf if math.isnan(sc[j]) else -float(sc[j]), j))
     k0 = max(0, min(int(k), nb))
     cum = np.cumsum(energy[order])
     total = max(float(energy.sum()), 1e-12)

@@ -90,6 +90,58 @@ def test_plan_resolve_rejects():
     assert "plan" in _lib.last_error()
 
 
+def _plan_doc_kinds():
+    """kind -> its paragraph in the bsg_plan comment of include/bsgemm.h."""
+    text = open(HEADER).read()
+    doc = text[text.index("/* Launch plan of the GEMM."):text.index("typedef struct bsg_plan")]
+    kinds = {}
+    cur = None
+    for line in doc.splitlines():
+        m = re.match(r"\s*\*\s{5}(\d)\s{2}(.*)", line)
+        if m:
+            cur = int(m.group(1))
+            kinds[cur] = m.group(2)
+        elif cur is not None and re.match(r"\s*\*\s{8}\S", line):
+            kinds[cur] += " " + line.split("*", 1)[1].strip()
+        else:
+            cur = None
+    return kinds
+
+
+def _accepted_kinds():
+    """Every kind bsg_plan_resolve resolves with at least one tile, probing each kind's row
+    counts with every other field left automatic."""
+    out = set()
+    for kind in range(0, 10):
+        for bt, rows in ((16, 16), (64, 64), (32, 32), (4, 4)):
+            if _resolve(bt, 4096, 64, 32, plan=_lib.Plan(0, 0, 0, 0, rows, kind))[0] == 0:
+                out.add(kind)
+                break
+    return out
+
+
+def test_header_documents_every_plan_kind():
+    """Each kind the library accepts has its own paragraph in the header's bsg_plan comment, the
+    header's split-K rule matches what the resolver enforces, and every kind the shipped plan
+    table names is among them (a C caller reading the header can form any shipped plan)."""
+    doc = _plan_doc_kinds()
+    accepted = _accepted_kinds() - {0}
+    assert accepted == {1, 2, 3, 4, 5, 6}
+    assert set(doc) == accepted, (sorted(doc), sorted(accepted))
+    for kind in accepted:
+        rows = 4 if kind == 3 else 16
+        rc_sk2 = _resolve(rows, 4096, 64, 32, plan=_lib.Plan(2, 0, 0, 0, rows, kind))[0]
+        single = "split_k must be 1" in doc[kind]
+        assert (rc_sk2 == _lib.BSG_ERR_UNSUPPORTED) == single, (kind, rc_sk2, doc[kind])
+    import json
+    table = json.load(open(os.path.join(ROOT, "towards-batched-activation-sparsity_amd", "bsa_mi355x",
+                                        "tuned_plans.json")))
+    shipped = {e["plan"][5] for e in table["entries"]}
+    assert shipped <= accepted and {5, 6} <= shipped
+    # the kind-0 heuristic stated in the header
+    assert _resolve(16, 4096, 64, 32)[1].kind == 1 and _resolve(64, 4096, 64, 32)[1].kind == 2
+
+
 def test_workspace_bytes():
     lib = bsa.load()
     p = _lib.Plan(1, 32, 4, 4, 16, 1)

@@ -109,6 +109,61 @@ def test_duplicate_ids_accumulate_twice(dev):
     assert_close(y, ref, "duplicates")
 
 
+def test_dropin_prepared_call_rechecks_what_its_key_does_not_pin(dev):
+    """A repeated drop-in call site takes a prepared launch (packed weight, plan and workspace of
+    its first call).  Every change its key does not pin must still be honoured: new x and out
+    tensors, a new list of the same length, an in-place weight update (re-pack), an x whose
+    address is not 16-byte aligned (copied on the general path), a non-contiguous out (raises),
+    and the unsorted / unsorted-as-given forms.  Each result is checked against the oracle."""
+    from bsa_mi355x import runtime
+
+    bt, k, n, na = 16, 11008, 4096, 86
+    x, w_nk, idx = case(61, bt, k, n, na, "laplace")
+    rng = np.random.default_rng(62)
+    idx_u = rng.permutation(idx).astype(np.int32)
+    wt = to_dev(w_nk, dev)
+    it = to_dev(idx_u, dev)
+    prefix = "prepared"
+
+    def run(xn, ids, out=None, sort=True):
+        xt = to_dev(xn, dev).view(bt, 1, k)
+        out = torch.full((bt, 1, n), float("nan"), dtype=F16, device=dev) if out is None else out
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(xt, wt, ids, out, cache_prefix=prefix,
+                                                            sort_active_blocks=sort)
+        torch.cuda.synchronize()
+        return out.view(bt, n).float().cpu().numpy()
+
+    runtime.forget_prepared_calls()
+    assert_close(run(x, it), orc.gemm_ref(x, w_nk, idx), "first call")
+    assert any(key[0] == prefix for key in runtime._PREPARED), "the first call left no prepared launch"
+    x2, _, _ = case(63, bt, k, n, 1, "laplace")
+    assert_close(run(x2, it), orc.gemm_ref(x2, w_nk, idx), "prepared: new x and out")
+    idx2 = np.sort(rng.choice(k // 64, na, replace=False)).astype(np.int32)
+    assert_close(run(x2, to_dev(rng.permutation(idx2).astype(np.int32), dev)), orc.gemm_ref(x2, w_nk, idx2),
+                 "prepared: new list")
+    with torch.no_grad():
+        wt.mul_(-0.5)
+    w_half = (w_nk.astype(np.float32) * -0.5).astype(np.float16)
+    assert_close(run(x2, it), orc.gemm_ref(x2, w_half, idx), "after an in-place weight update")
+    # the same shape and strides at an address 8 bytes past 16-byte alignment
+    base = torch.empty(bt * k + 4, dtype=F16, device=dev)
+    xo = base[4:].view(bt, 1, k)
+    xo.copy_(to_dev(x, dev).view(bt, 1, k))
+    assert xo.data_ptr() % 16 == 8
+    out = torch.full((bt, 1, n), float("nan"), dtype=F16, device=dev)
+    bsa._prepacked_block_sparse_gemm_from_active_blocks(xo, wt, it, out, cache_prefix=prefix)
+    torch.cuda.synchronize()
+    assert_close(out.view(bt, n).float().cpu().numpy(), orc.gemm_ref(x, w_half, idx), "unaligned x")
+    big = torch.empty(bt, 2, n, dtype=F16, device=dev)
+    run(x, it)
+    with pytest.raises(ValueError):
+        bsa._prepacked_block_sparse_gemm_from_active_blocks(to_dev(x, dev).view(bt, 1, k), wt, it, big[:, :1, :],
+                                                            cache_prefix=prefix)
+    # a list taken as given (no sort): the kernel sums in list order, the same blocks
+    assert_close(run(x, it, sort=False), orc.gemm_ref(x, w_half, idx_u), "unsorted as given")
+    assert_close(run(x, it, sort=False), orc.gemm_ref(x, w_half, idx_u), "unsorted as given, prepared")
+
+
 def test_every_instantiated_tile(dev):
     """Every compiled (rows, cols, waves, depth) kernel, split-K 1 and 3 (kind 3: 1 only), fp16
     and bf16; bt=37 gives kind 3 (at most 8 rows per work-group) several row groups."""

@@ -192,6 +192,64 @@ def test_self_scored_selection_in_one_launch(dev, bt, kdim, n, k, plan):
         assert torch.count_nonzero(y).item() == 0
 
 
+@pytest.mark.parametrize("bt,kdim,n,k,plan", [(3, 4096, 1024, 13, (1, 16, 4, 4, 16, 6)),
+                                              (8, 1536, 4096, 11, (1, 48, 4, 4, 16, 5)),
+                                              (2, 4096, 512, 5, (1, 16, 2, 4, 16, 1))])
+def test_self_scored_selection_with_inf_and_nan(dev, bt, kdim, n, k, plan):
+    """Non-finite activations on the one-launch path: the self-scored sums take the integer units
+    for a group holding Inf or NaN (both above every finite value, NaN above Inf), which must
+    rank exactly as the score launch's integer sums and the oracle do.  One +Inf and one NaN sit
+    in different blocks and rows; the count and ids must equal the oracle's and the two-launch
+    selector's (bsg_select_topk_l1) on the same x.  Y agrees with the GEMM on the same list: the
+    same non-finite positions, and bit for bit (and within tolerance of the oracle) on the rows
+    that hold neither value."""
+    import ctypes
+
+    from bsa_mi355x import _lib
+    from bsa_mi355x.runtime import _stream_handle
+
+    x, w_nk, _ = case(1700 + bt + k, bt, kdim, n, 1, "normal")
+    nb = -(-kdim // 64)
+    inf_row, inf_blk, nan_row, nan_blk = 0, 5, bt - 1, 9
+    x[inf_row, 64 * inf_blk + 3] = np.float16(np.inf)
+    x[nan_row, 64 * nan_blk + 7] = np.float16(np.nan)
+    want = orc.select_topk_l1(x, k)
+    assert inf_blk in want and nan_blk in want
+    lib = bsa.load()
+    xt = to_dev(x, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    pl = bsa.Plan(*plan)
+    sel = int(lib.bsg_select_workspace_bytes(kdim))
+    gws = int(lib.bsg_gemm_workspace_bytes(bt, n, ctypes.byref(pl)))
+    ws = torch.zeros(sel + gws, dtype=torch.uint8, device=dev)
+    ws[256:sel] = 0xAB
+    y = torch.full((bt, n), 1.0, dtype=torch.float16, device=dev)
+    idx = torch.full((k,), -1, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    print(f"self-scored select+gemm with Inf/NaN bt={bt} K={kdim} N={n} k={k} plan={plan}", flush=True)
+    rc = lib.bsg_select_gemm(xt.data_ptr(), kdim, bt, kdim, k, packed.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(),
+                             y.data_ptr(), n, 0, ws.data_ptr(), sel + gws, ctypes.byref(pl), _stream_handle(dev))
+    assert rc == _lib.BSG_OK, _lib.last_error()
+    torch.cuda.synchronize()
+    assert bool((ws[256:sel] == 0xAB).all()), "a score launch ran: the case is not the one-launch path"
+    c = int(cnt.item())
+    assert c == len(want) == min(k, nb)
+    assert np.array_equal(idx.cpu().numpy()[:c], want)
+    two_idx, two_cnt = _select(dev, x, k)
+    assert two_cnt == c and np.array_equal(two_idx[:two_cnt], want)
+    y_list = torch.full((bt, n), 1.0, dtype=torch.float16, device=dev)
+    bsa.gemm_packed(xt, packed, n, to_dev(want.astype(np.int32), dev), y_list, num_active=c, plan=pl,
+                    workspace_prefix="t_self_nonfinite")
+    torch.cuda.synchronize()
+    assert torch.equal(torch.isnan(y), torch.isnan(y_list)) and torch.equal(torch.isinf(y), torch.isinf(y_list))
+    assert bool(torch.isnan(y[nan_row]).all())
+    finite_rows = [r for r in range(bt) if r not in (inf_row, nan_row)]
+    if finite_rows:
+        assert torch.equal(y[finite_rows], y_list[finite_rows])
+        assert_close(y[finite_rows].float().cpu().numpy(), orc.gemm_ref(x[finite_rows], w_nk, want),
+                     f"finite rows bt={bt} K={kdim}")
+
+
 def test_two_launch_selection_above_the_self_scoring_size(dev):
     """Above 24 KiB of activations (bt x K x 2) or 8 rows, and on the dot-product kernel (kind 3),
     the score launch runs, writing the block scores into the selector's part of the workspace."""
@@ -344,3 +402,131 @@ def test_reference_drop_ins_ignore_a_prior_of_the_wrong_length(dev):
     want, _, _ = orc.select_scored_ref(x, orc.n_keep(0.3, 64), "l2_mean", prior=prior.cpu().numpy())
     assert np.array_equal(got, want) and not np.array_equal(got, base)
 
+
+
+# ---------------------------------------------------------------------------------------
+# Selection by the reference's rules + GEMM in one library call (bsg_select_gemm_rule): the
+# kept ids, count and ratio must be select_topk's (and the float64 oracle's) for the same x and
+# options, and Y the GEMM on that list.
+
+
+def _rule_call(dev, x, w_nk, k, dtype=torch.float16, plan=None, **kw):
+    from bsa_mi355x.select import select_gemm_rule_packed
+
+    kw = {n: (to_dev(np.asarray(v, np.float32), dev, torch.float32) if isinstance(v, np.ndarray) else v)
+          for n, v in kw.items()}
+    bt, kdim = x.shape
+    n = w_nk.shape[0]
+    xt = torch.from_numpy(np.asarray(x, np.float32)).to(dtype).to(dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev, dtype))
+    y = torch.full((bt, n), float("nan"), dtype=dtype, device=dev)
+    print(f"rule select+gemm bt={bt} K={kdim} N={n} k={k} {dtype} plan={plan} opts={sorted(kw)}", flush=True)
+    idx, cnt, ratio = select_gemm_rule_packed(xt, packed, n, k, y, plan=plan, **kw)
+    torch.cuda.synchronize()
+    c = int(cnt.item())
+    sel_idx, sel_cnt, sel_ratio = bsa.select_topk(xt, k, **kw)
+    torch.cuda.synchronize()
+    return (idx[:c].cpu().numpy(), c, None if ratio is None else float(ratio.item()), y, xt, packed,
+            (sel_idx[:int(sel_cnt.item())].cpu().numpy(), int(sel_cnt.item()),
+             None if sel_ratio is None else float(sel_ratio.item())))
+
+
+@pytest.mark.parametrize("bt,kdim,n,k", [(16, 4096, 4096, 23), (64, 4096, 11008, 31), (64, 11008, 4096, 83)])
+@pytest.mark.parametrize("score,prior,scale", [("l2_mean", False, False), ("l2_mean", True, False),
+                                               ("energy", False, True), ("energy", True, False)])
+def test_rule_select_gemm_matches_selector_and_oracle(dev, bt, kdim, n, k, score, prior, scale):
+    """The reference's decode linear (select -> GEMM, RRD:179-284) as one call at the shapes of
+    BASELINE's batches: ids and count equal the oracle's (select_scored_ref) and the separate
+    selector's; Y is within tolerance of gemm_ref on those blocks and bit for bit the GEMM on
+    the same list with the same plan."""
+    rng = np.random.default_rng(bt * 7 + k)
+    x = rng.laplace(0, 0.05, size=(bt, kdim)).astype(np.float16)
+    w_nk = (rng.normal(0, 0.02, size=(n, kdim))).astype(np.float16)
+    nb = kdim // 64
+    kw = dict(score=score)
+    if prior:
+        kw.update(block_prior=rng.uniform(0, 1, size=nb).astype(np.float32), prior_alpha=0.7, prior_eps=0.1)
+    if scale:
+        kw["channel_scale"] = rng.uniform(0.5, 2, size=kdim).astype(np.float32)
+    got, c, _, y, xt, packed, (s_idx, s_cnt, _) = _rule_call(dev, x, w_nk, k, **kw)
+    want, keep, _ = orc.select_scored_ref(x, k, score, prior=kw.get("block_prior"), alpha=0.7, eps=0.1,
+                                          scale=kw.get("channel_scale"))
+    assert c == keep == min(k, nb) and np.array_equal(got, want)
+    assert s_cnt == c and np.array_equal(s_idx, want)
+    assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), f"rule {score} bt={bt} K={kdim}")
+    pl = bsa.resolve_plan(bt, n, -(-kdim // 64), min(k, nb), dev, None, select=True)
+    y_list = torch.full_like(y, float("nan"))
+    bsa.gemm_packed(xt, packed, n, to_dev(want.astype(np.int32), dev), y_list, num_active=c, plan=pl,
+                    workspace_prefix="t_rule_ref")
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_list)
+
+
+def test_rule_select_gemm_three_launch_forms_and_edges(dev):
+    """The forms that rank in a separate launch (an energy budget with its ratio, bf16, a
+    dot-product plan) give the selector's ids, count and ratio too; a partial last K-block is
+    never kept (floor(K/64) scored blocks), k above the block count keeps every scored block,
+    k = 0 writes zeros, and negative scores (a negative channel scale) rank below the rest."""
+    rng = np.random.default_rng(5)
+    # energy budget + ratio: three launches, the GEMM on the device count
+    x = rng.laplace(0, 0.05, size=(16, 4096)).astype(np.float16)
+    w_nk = rng.normal(0, 0.02, size=(1024, 4096)).astype(np.float16)
+    got, c, ratio, y, _, _, (s_idx, s_cnt, s_ratio) = _rule_call(dev, x, w_nk, 8, score="energy", energy_keep=0.6)
+    want, keep, wratio = orc.select_scored_ref(x, 8, "energy", energy_keep=0.6)
+    assert c == keep == s_cnt and keep > 8 and np.array_equal(got, want) and np.array_equal(s_idx, want)
+    assert ratio == s_ratio and abs(ratio - wratio) <= 1e-6
+    assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), "energy budget")
+    # bf16
+    xb = rng.normal(0, 1, size=(16, 4096)).astype(np.float32)
+    xb16 = torch.from_numpy(xb).to(torch.bfloat16).float().numpy()
+    wb = rng.normal(0, 0.02, size=(512, 4096)).astype(np.float32)
+    wb16 = torch.from_numpy(wb).to(torch.bfloat16).float().numpy()
+    got, c, _, y, _, _, (s_idx, _, _) = _rule_call(dev, xb, wb, 20, dtype=torch.bfloat16, score="l2_mean")
+    want, _, _ = orc.select_scored_ref(xb16, 20, "l2_mean")
+    assert c == 20 and np.array_equal(got, want) and np.array_equal(s_idx, want)
+    ref = orc.gemm_ref(xb16.astype(np.float32), wb16.astype(np.float32), want)
+    yb = y.float().cpu().numpy()
+    assert orc.rel_frobenius(yb, ref) <= 5e-3
+    # a dot-product (kind 3) plan at 4 rows: no selection instantiation, rank launch
+    x4 = rng.laplace(0, 0.05, size=(4, 4096)).astype(np.float16)
+    got, c, _, y, _, _, (s_idx, _, _) = _rule_call(dev, x4, w_nk, 13, plan=bsa.Plan(1, 16, 4, 4, 4, 3),
+                                                   score="l2_mean")
+    want, _, _ = orc.select_scored_ref(x4, 13, "l2_mean")
+    assert c == 13 and np.array_equal(got, want) and np.array_equal(s_idx, want)
+    assert_close(y.float().cpu().numpy(), orc.gemm_ref(x4, w_nk, want), "kind 3 plan")
+    # K tail: 15 scored blocks of 16; k past them keeps the 15 scored blocks only
+    xt_ = rng.laplace(0, 0.05, size=(16, 1000)).astype(np.float16)
+    xt_[:, 960:] = 30.0  # the partial block would win if it were scored
+    wt_ = rng.normal(0, 0.02, size=(256, 1000)).astype(np.float16)
+    got, c, _, y, _, _, _ = _rule_call(dev, xt_, wt_, 40, score="l2_mean")
+    assert c == 15 and np.array_equal(got, np.arange(15))
+    assert_close(y.float().cpu().numpy(), orc.gemm_ref(xt_, wt_, np.arange(15)), "K tail")
+    got, c, _, y, _, _, _ = _rule_call(dev, xt_, wt_, 6, score="energy")
+    want, _, _ = orc.select_scored_ref(xt_, 6, "energy")
+    assert c == 6 and np.array_equal(got, want) and 15 not in got
+    # k = 0: nothing kept, zeros
+    got, c, _, y, _, _, _ = _rule_call(dev, x, w_nk, 0, score="l2_mean")
+    assert c == 0 and torch.count_nonzero(y).item() == 0
+    # negative channel scale: odd blocks score below zero
+    scale = np.where(np.arange(4096) // 64 % 2 == 0, 1.0, -1.0).astype(np.float32)
+    for k in (20, 40):
+        got, c, _, y, _, _, (s_idx, _, _) = _rule_call(dev, x, w_nk, k, score="energy", channel_scale=scale)
+        want, _, _ = orc.select_scored_ref(x, k, "energy", scale=scale)
+        assert c == k and np.array_equal(got, want) and np.array_equal(s_idx, want), k
+        assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), f"negative scale k={k}")
+
+
+def test_rule_select_gemm_ranks_a_nan_block_first(dev):
+    """A NaN activation makes its block's score NaN, which ranks above every number (as
+    torch.topk ranks NaN); ties between equal scores still go to the lower block id."""
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, size=(16, 4096)).astype(np.float16)
+    x[3, 64 * 40 + 9] = np.float16(np.nan)
+    for j in (10, 20, 30):
+        x[:, 64 * j:64 * j + 64] = 40.0
+    w_nk = rng.normal(0, 0.02, size=(512, 4096)).astype(np.float16)
+    for score in ("l2_mean", "energy"):
+        got, c, _, _, _, _, (s_idx, _, _) = _rule_call(dev, x, w_nk, 3, score=score)
+        want, _, _ = orc.select_scored_ref(x, 3, score)
+        assert c == 3 and np.array_equal(got, [10, 20, 40]) and np.array_equal(want, [10, 20, 40])
+        assert np.array_equal(s_idx, want)

@@ -237,6 +237,26 @@ def test_prior_of_the_wrong_length_is_ignored():
     assert np.array_equal(ids, [2, 3])
 
 
+def test_scored_ref_ranks_nan_first_and_negative_scores_last_like_torch():
+    """A block whose score is NaN ranks above every number, as torch.topk ranks NaN (the
+    reference's own call, RRD:113), and negative scores (a negative channel scale) rank below
+    zero and positive ones: the float64 restatement agrees with the torch float32 one."""
+    rng = np.random.default_rng(31)
+    x = rng.normal(0, 1, size=(4, 8 * 64)).astype(np.float16)
+    x[2, 64 * 5 + 7] = np.nan
+    for score in ("l2_mean", "energy"):
+        ids, keep, _ = orc.select_scored_ref(x, 3, score)
+        ids32, keep32, _ = orc.select_scored_torch32(x, 3, score)
+        assert 5 in ids and keep == keep32 == 3 and np.array_equal(ids, ids32), (score, ids, ids32)
+    xf = rng.normal(0, 1, size=(4, 8 * 64)).astype(np.float16)
+    scale = np.where(np.arange(8 * 64) // 64 % 2 == 0, 1.0, -1.0).astype(np.float32)  # odd blocks score < 0
+    for k in (3, 5):
+        ids, _, _ = orc.select_scored_ref(xf, k, "energy", scale=scale)
+        ids32, _, _ = orc.select_scored_torch32(xf, k, "energy", scale=scale)
+        assert np.array_equal(ids, ids32)
+    assert np.array_equal(orc.select_scored_ref(xf, 4, "energy", scale=scale)[0], [0, 2, 4, 6])
+
+
 def test_make_inputs_several_masks_equal_single_draws():
     """A list of counts gives, for each, the mask make_inputs draws for that count alone."""
     x, w, masks = orc.make_inputs(77, 3, 640, 48, "laplace", na=[2, 5, 10])

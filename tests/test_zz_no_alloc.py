@@ -25,8 +25,13 @@ def _inputs(dev, seed, bt, k, n):
     return x, np.ascontiguousarray(w_kn.T), to_dev(x, dev), packed
 
 
+_NOALLOC_CALLS = [0]  # bsg_select_gemm_noalloc calls made by this module (no other module makes any)
+
+
 def _call(dev, fn_name, xt, packed, n, k, plan, ws=None):
     lib = bsa.load()
+    if fn_name != "bsg_select_gemm":
+        _NOALLOC_CALLS[0] += 1
     bt, kd = xt.shape
     nblk = (kd + 63) // 64
     idx = torch.full((max(1, min(k, nblk)),), -1, dtype=torch.int32, device=dev)
@@ -55,6 +60,51 @@ def _workspace(dev, bt, k, n, keep, plan):
     assert lib.bsg_plan_resolve(bt, n, nblk, min(keep, nblk), cu, ctypes.byref(pl)) == 0
     nbytes = lib.bsg_select_workspace_bytes(k) + lib.bsg_gemm_workspace_bytes(bt, n, ctypes.byref(pl))
     return torch.zeros(int(nbytes), dtype=torch.uint8, device=dev)
+
+
+def test_first_noalloc_call_is_made_inside_graph_capture(dev):
+    """The process's first bsg_select_gemm_noalloc call (defined first in the only module that
+    calls it) is made while torch.cuda.graph captures its side stream: the scratch lookup runs
+    under capture and the counter clear is recorded into the graph.  Every replay, with the
+    program's own eager work (another allocation-free call sharing the scratch, a smaller one)
+    and a synchronisation between replays, must give the eager workspace entry point's ids,
+    count and Y bit for bit."""
+    if _NOALLOC_CALLS[0] != 0:
+        pytest.skip("an allocation-free call already ran in this process")
+    lib = bsa.load()
+    bt, k, n, keep = 16, 11008, 4096, 62
+    plan = (2, 16, 2, 4, 16, 1)  # split-K: the graph's GEMM uses the scratch's counters and partials
+    x, w_nk, xt, packed = _inputs(dev, 12, bt, k, n)
+    idx = torch.full((keep,), -1, dtype=torch.int32, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    y = torch.full((bt, n), float("nan"), dtype=torch.float16, device=dev)
+    pl = _lib.Plan(*plan)
+    torch.cuda.synchronize()
+    print(f"noalloc first call under capture bt={bt} K={k} N={n} k={keep} plan={plan}", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _NOALLOC_CALLS[0] += 1
+        rc = lib.bsg_select_gemm_noalloc(xt.data_ptr(), k, bt, k, keep, packed.data_ptr(), n, idx.data_ptr(),
+                                         cnt.data_ptr(), y.data_ptr(), n, _lib.BSG_F16, ctypes.byref(pl),
+                                         torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    i0, c0, y0 = _call(dev, "bsg_select_gemm", xt, packed, n, keep, plan, ws=_workspace(dev, bt, k, n, keep, plan))
+    want = orc.select_topk_l1(x, keep)
+    assert int(c0.item()) == len(want) == keep and np.array_equal(i0.cpu().numpy(), want)
+    _, _, xs, packed_s = _inputs(dev, 13, 2, 4096, 1024)
+    for r in range(3):
+        idx.fill_(-1)
+        cnt.fill_(-1)
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(cnt.item()) == keep, r
+        assert torch.equal(idx, i0), r
+        assert torch.equal(y.view(torch.int16), y0.view(torch.int16)), r
+        _call(dev, "bsg_select_gemm_noalloc", xs, packed_s, 1024, 13, (2, 16, 2, 4, 16, 1))
+    assert_close(y.float().cpu().numpy(), orc.gemm_ref(x, w_nk, want), "noalloc under capture")
+    del g
 
 
 # (bt, K, N, k, plan): split-K plans so the scratch's counters and partials are exercised; the

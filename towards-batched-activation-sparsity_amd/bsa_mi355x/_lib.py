@@ -128,6 +128,8 @@ SIGNATURES = {
                                _i64, _vp]),
     "bsg_select_gemm": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int, _vp, _i64,
                                _pplan, _vp]),
+    "bsg_select_gemm_rule": (_int, [_vp, _i64, _i64, _i64, _i32, ctypes.POINTER(SelectOpts), _vp, _i64, _vp, _vp,
+                                    _vp, _i64, _int, _vp, _i64, _pplan, _vp]),
     "bsg_select_gemm_noalloc": (_int, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _int,
                                        _pplan, _vp]),
     "bsg_read_calibrate": (_int, [_vp, _i64, _vp, _vp]),

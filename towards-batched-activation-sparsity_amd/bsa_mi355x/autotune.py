@@ -52,12 +52,15 @@ def enabled() -> bool:
 def set_autotune(enabled: bool = True, cache_path: Optional[str] = None) -> None:
     """Turn first-call tuning on or off; with cache_path, load tuned keys from that JSON file
     (when it exists) and write every new one back to it."""
+    from .runtime import forget_prepared_calls
+
     with _LOCK:
         _STATE["enabled"] = bool(enabled)
         if cache_path is not None:
             _STATE["path"] = cache_path
             _STATE["loaded"] = False
     _load()
+    forget_prepared_calls()
 
 
 def stats() -> dict:
@@ -66,10 +69,13 @@ def stats() -> dict:
 
 
 def clear() -> None:
+    from .runtime import forget_prepared_calls
+
     with _LOCK:
         _CACHE.clear()
         _STATE["tunes"] = 0
         _STATE["timed_launches"] = 0
+    forget_prepared_calls()
 
 
 def cached(k: Key) -> Optional[Plan]:

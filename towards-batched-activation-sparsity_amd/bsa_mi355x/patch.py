@@ -9,7 +9,12 @@ switches by importing them.  Behaviour kept from the reference:
   * a call with more than one token per sequence (prefill), or a density >= 1, runs the
     module's dense `F.linear` (the dense-prefill bypass);
   * a decode call selects blocks with the reference's rules (`_select_active_blocks`) and runs
-    the GEMM kernel family its lookup-table entry names (naive / bpl, split-K, tile);
+    the GEMM on them.  By default both are one library call (bsg_select_gemm_rule: the score
+    launch, then a GEMM whose work-groups rank the scores themselves), with the plan of the
+    lookup-table entry (its split-K and tile; naive and bpl sum the kept blocks in the same
+    ascending order here).  With profile_sparse_parts (the reference times selection and GEMM
+    apart) or fixed masks, selection and GEMM run as separate calls, the GEMM through the kernel
+    family the entry names (naive / bpl, split-K, tile), as in RRD:207-276;
   * the optional energy gate (modes dense / expand / scaled / hybrid), mask reuse, per-step
     density schedules and weight-aware scores behave as there.
 
@@ -24,12 +29,14 @@ from typing import Dict, List, Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from .runtime import (INDEX_BLOCK_META_SIZE, _build_active_k_bitmap, _get_prepacked_weight_block_major,
-                      _prepacked_block_sparse_gemm_from_active_blocks,
+from .runtime import (INDEX_BLOCK_META_SIZE, _build_active_k_bitmap, _check_shapes, _get_prepacked_weight_block_major,
+                      _packed_entry, _prepacked_block_sparse_gemm_from_active_blocks,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload_splitk,
-                      _prepacked_block_sparse_gemm_from_active_blocks_splitk)
-from .select import _energy_expanded_active_blocks, _select_active_blocks, _topk_energy_ratio
+                      _prepacked_block_sparse_gemm_from_active_blocks_splitk, _views, make_plan,
+                      n_keep_for_density)
+from .select import (_energy_expanded_active_blocks, _prior_or_none, _select_active_blocks, _topk_energy_ratio,
+                     select_gemm_rule_packed)
 
 PROJS = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
 PROJ_TO_SHAPE = {"q_proj": "qkvo", "k_proj": "qkvo", "v_proj": "qkvo", "o_proj": "qkvo",
@@ -76,6 +83,12 @@ def _sparse_linear(x, weight, density: float, cfg: dict, cache_prefix: str, bloc
         return F.linear(x, weight)
     n_out, d_in = int(weight.shape[0]), int(weight.shape[1])
     total_k = d_in // block_k
+    if fixed_active_blocks is None and not profile_sparse_parts:
+        out = torch.empty(x3.shape[0], x3.shape[1], n_out, device=x3.device, dtype=x3.dtype)
+        _fused_select_linear(x3, weight, out, density, cfg, cache_prefix, block_k, block_prior, prior_alpha,
+                             prior_eps, block_score_scale)
+        stats["calls"] += 1
+        return out.reshape(x.shape[0], n_out) if x.dim() == 2 else out
 
     t0 = _sync_time(profile_sparse_parts)
     if fixed_active_blocks is not None:
@@ -119,6 +132,34 @@ def _sparse_linear(x, weight, density: float, cfg: dict, cache_prefix: str, bloc
         stats["wall_s"] += dt
         stats["kernel_wall_s"] = stats.get("kernel_wall_s", 0.0) + dt
     return out.reshape(x.shape[0], n_out) if x.dim() == 2 else out
+
+
+def _fused_select_linear(x3, weight, out, density: float, cfg: dict, cache_prefix: str, block_k: int,
+                         block_prior, prior_alpha: float, prior_eps: float, block_score_scale) -> None:
+    """The reference's selection (`_select_active_blocks`, RRD:90-113: mean L2 norm, or the
+    channel-scaled energy with block_score_scale; the prior when it has floor(K/64) entries;
+    n_keep = max(1, min(nblk, round(density * nblk)))) and the GEMM on the kept blocks, as one
+    library call on the packed weight of `cache_prefix` (the select -> bitmap -> GEMM of
+    RRD:207-276 without the host-side steps between them).  The lookup row's split-K and tile
+    become the plan; a naive row without split-K takes the tuned table's plan."""
+    if int(block_k) != INDEX_BLOCK_META_SIZE:
+        raise ValueError(f"block_k must be {INDEX_BLOCK_META_SIZE}")
+    n_out = out.shape[-1]
+    x2d, y2d, bt, d_in = _views(x3, out, n_out)
+    _check_shapes(x2d, weight, y2d, n_out, d_in)
+    split_k = int(cfg.get("best_K") or 1)
+    tb, tn, nw, ns = cfg.get("best_tile") or [None, None, None, None]
+    plan = None
+    if str(cfg["best_kern"]) != "naive" or split_k > 1:
+        plan = make_plan(split_k if split_k > 1 else None, tb, tn, nw, ns, bt=bt)
+        if not any(plan.as_tuple()):
+            plan = None
+    entry = _packed_entry(weight, block_k, cache_prefix)
+    select_gemm_rule_packed(x2d, entry.packed, n_out, n_keep_for_density(density, d_in // block_k), y2d,
+                            score="energy" if block_score_scale is not None else "l2_mean",
+                            block_prior=_prior_or_none(block_prior, x2d), prior_alpha=prior_alpha,
+                            prior_eps=prior_eps, channel_scale=block_score_scale, plan=plan,
+                            workspace_prefix=f"{cache_prefix}_selrule_ws")
 
 
 class _SparseForward:

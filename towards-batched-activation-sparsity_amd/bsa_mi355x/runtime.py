@@ -165,10 +165,13 @@ def _get_prepacked_weight_block_major(weight: torch.Tensor, block_k: int, cache_
 
 
 def release_prepacked_weights(cache_prefix: Optional[str] = None) -> None:
-    """Drop cached packed weights (all prefixes, or one)."""
+    """Drop cached packed weights (all prefixes, or one), and the prepared drop-in calls that
+    hold them."""
     for name, cache in list(_WEIGHT_PREPACK_CACHE.items()):
         if isinstance(cache, dict) and (cache_prefix is None or name == cache_prefix):
             cache.clear()
+    for key in [k for k in _PREPARED if cache_prefix is None or k[0] == cache_prefix]:
+        del _PREPARED[key]
 
 
 # ---------------------------------------------------------------------------------------
@@ -344,7 +347,9 @@ def gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, active_bloc
     Exactly one source of active blocks: `active_blocks` (int32 device list, host length or
     `num_active`; optional device count), `bitmap` (u8), or neither (dense: every block).
     sort_list: the GEMM sorts the list ascending itself (bsg_gemm_sorted, at most
-    MAX_NBLK // 2 entries), with the result of an ascending sort followed by the GEMM."""
+    MAX_NBLK // 2 entries), with the result of an ascending sort followed by the GEMM.  With
+    `num_active_dev` the device count is applied first: only the first min(count, num_active)
+    entries are sorted and used (the GEMM on sort(list[:count]), not on the count smallest ids)."""
     lib = load()
     dev = _require_cuda(x2d, packed, y2d)
     code = _dtype_code(x2d)
@@ -468,6 +473,72 @@ def _sort_active_blocks_asc(active_blocks: torch.Tensor) -> torch.Tensor:
     return torch.sort(active_blocks.contiguous())[0].contiguous()
 
 
+class _PreparedCall:
+    """One eager call site of the drop-in, resolved once: the launch arguments that depend only on
+    the problem (packed weight, plan, workspace, sizes), kept with references to the packed weight
+    and the workspace so that neither is freed while the entry lives.  A hit re-checks only what
+    the key does not pin (the weight's identity, storage and version; alignment and contiguity; the
+    current device) and passes the call's own pointers and stream."""
+
+    __slots__ = ("wref", "wptr", "wver", "fn", "wp", "ldx", "bt", "kd", "n", "na", "ldy", "code", "ws", "ws_bytes",
+                 "plan", "plan_ref", "dev_index", "keep", "kernel")
+
+    def launch(self, x: torch.Tensor, ab: torch.Tensor, out: torch.Tensor) -> None:
+        rc = self.fn(x.data_ptr(), self.ldx, self.bt, self.kd, self.wp, self.n, ab.data_ptr(), self.na, None,
+                     out.data_ptr(), self.ldy, self.code, self.ws, self.ws_bytes, self.plan_ref,
+                     torch._C._cuda_getCurrentRawStream(self.dev_index))
+        if rc != _lib.BSG_OK:
+            check(rc)
+        self.kernel.last_plan = self.plan
+
+
+_PREPARED: Dict[tuple, _PreparedCall] = {}
+_PREPARED_MAX = 4096
+
+
+def forget_prepared_calls() -> None:
+    """Drop every prepared drop-in call (their plans came from tuning state that is being reset)."""
+    _PREPARED.clear()
+
+
+def _prepared_key(x, weight, active_blocks, out, cache_prefix, sort_active_blocks, active_blocks_limit) -> tuple:
+    return (cache_prefix, id(weight), x.shape, x.stride(), x.dtype, x.get_device(), out.shape, out.dtype,
+            out.get_device(), active_blocks.shape, active_blocks.dtype, active_blocks.get_device(),
+            sort_active_blocks, active_blocks_limit)
+
+
+def _prepare_call(key, x, weight, entry, active_blocks, out, x2d, y2d, num_blocks, sort_list, pl, ws_prefix) -> None:
+    """Record the call just launched through the general path, when its form needs no per-call
+    work: no copy of x, an int32 contiguous list passed as given (the caller excludes a list sorted
+    by a torch.sort launch), not under capture (where first-call tuning is deferred)."""
+    if (torch.cuda.is_current_stream_capturing() or x2d.data_ptr() != x.data_ptr() or not x.is_contiguous()
+            or active_blocks.dtype != torch.int32 or not active_blocks.is_contiguous()):
+        return
+    lib = load()
+    code = _dtype_code(x2d)
+    ws_bytes = int(lib.bsg_gemm_workspace_bytes(x2d.shape[0], y2d.shape[1], ctypes_byref(pl)))
+    ws = (_workspace(ws_prefix, x2d.device, ws_bytes, (x2d.shape[0], y2d.shape[1]) + pl.as_tuple())
+          if ws_bytes > 0 else None)
+    c = _PreparedCall()
+    c.wref = entry.ref
+    c.wptr = int(weight.data_ptr())
+    c.wver = entry.version
+    c.fn = lib.bsg_gemm_sorted if sort_list else lib.bsg_gemm
+    c.wp = int(entry.packed.data_ptr())
+    c.ldx, c.bt, c.kd = int(x2d.stride(0)), int(x2d.shape[0]), int(x2d.shape[1])
+    c.n, c.na, c.ldy, c.code = int(y2d.shape[1]), int(num_blocks), int(y2d.stride(0)), code
+    c.ws = ws.data_ptr() if ws is not None else None
+    c.ws_bytes = ws_bytes
+    c.plan = Plan(*pl.as_tuple())
+    c.plan_ref = ctypes_byref(c.plan)
+    c.dev_index = x2d.device.index if x2d.device.index is not None else torch.cuda.current_device()
+    c.keep = (entry.packed, ws)
+    c.kernel = prepacked_block_sparse_gemm_batched_kernel
+    if len(_PREPARED) >= _PREPARED_MAX:
+        _PREPARED.clear()
+    _PREPARED[key] = c
+
+
 def _prepacked_block_sparse_gemm_from_active_blocks(
     x: torch.Tensor,
     weight: torch.Tensor,
@@ -483,7 +554,21 @@ def _prepacked_block_sparse_gemm_from_active_blocks(
 
     `active_blocks_limit` keeps the first that many list entries (KRN:3179, 3191-3192);
     `use_run_compressed` and `proj_tag` only selected Triton metadata variants and are
-    accepted for signature compatibility (the HIP kernel streams the list as given)."""
+    accepted for signature compatibility (the HIP kernel streams the list as given).
+
+    A repeated call site (same weight, shapes, dtypes, devices and options) takes a prepared
+    launch: the packed weight, plan and workspace resolved by its first call, with only the
+    weight's identity and version, the alignment and contiguity of x, out and the list, and the
+    current device re-checked before the one library call."""
+    key = _prepared_key(x, weight, active_blocks, out, cache_prefix, sort_active_blocks, active_blocks_limit)
+    pc = _PREPARED.get(key)
+    if pc is not None:
+        if (pc.wref() is weight and weight._version == pc.wver and weight.data_ptr() == pc.wptr
+                and x.data_ptr() % 16 == 0 and out.is_contiguous() and active_blocks.is_contiguous()
+                and torch._C._cuda_getDevice() == pc.dev_index):
+            pc.launch(x, active_blocks, out)
+            return
+        del _PREPARED[key]
     n_dim = out.shape[-1]
     num_blocks = int(active_blocks.numel()) if active_blocks_limit is None else int(active_blocks_limit)
     num_blocks = min(num_blocks, int(active_blocks.numel()))
@@ -502,9 +587,12 @@ def _prepacked_block_sparse_gemm_from_active_blocks(
     in_kernel = sort_active_blocks and num_blocks <= MAX_NBLK // 2
     if sort_active_blocks and not in_kernel:
         ab = _sort_active_blocks_asc(ab[:num_blocks])
-    gemm_packed(x2d, entry.packed, n_dim, ab, y2d, num_active=num_blocks, plan=None,
-                workspace_prefix=f"{cache_prefix}_ws", kernel=prepacked_block_sparse_gemm_batched_kernel,
-                sort_list=in_kernel)
+    pl = gemm_packed(x2d, entry.packed, n_dim, ab, y2d, num_active=num_blocks, plan=None,
+                     workspace_prefix=f"{cache_prefix}_ws", kernel=prepacked_block_sparse_gemm_batched_kernel,
+                     sort_list=in_kernel)
+    if ab is active_blocks and (in_kernel or not sort_active_blocks):
+        _prepare_call(key, x, weight, entry, active_blocks, out, x2d, y2d, num_blocks, in_kernel, pl,
+                      f"{cache_prefix}_ws")
 
 
 def _prepacked_block_sparse_gemm_from_active_blocks_splitk(

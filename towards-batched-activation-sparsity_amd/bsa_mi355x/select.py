@@ -85,6 +85,33 @@ def _prior_or_none(block_prior: Optional[torch.Tensor], x: torch.Tensor) -> Opti
     return block_prior
 
 
+def _capacity(score: str, k: int, kd: int, energy_keep: float) -> int:
+    """Entries the kept list may hold: every scored block (floor(K/64)) under an energy budget,
+    else min(k, blocks) (ceil(K/64) blocks for the L1 rule, floor(K/64) for the reference's)."""
+    nb = kd // BLOCK_K
+    if score == "l1":
+        return max(0, min(int(k), (kd + BLOCK_K - 1) // BLOCK_K))
+    return nb if energy_keep > 0 else max(0, min(int(k), nb))
+
+
+def _rule_opts(dev, kd: int, score: str, block_prior, prior_alpha: float, prior_eps: float, channel_scale,
+               energy_keep: float, ratio_out: Optional[torch.Tensor]):
+    """bsg_select_opts for a call, the ratio output (made when an energy budget is set and none
+    was given) and the device tensors the options point at (kept alive by the caller)."""
+    if score not in _SCORES:
+        raise ValueError(f"score must be one of {sorted(_SCORES)}")
+    want_ratio = ratio_out is not None or (score != "l1" and energy_keep > 0)
+    if want_ratio and ratio_out is None:
+        ratio_out = torch.empty(1, dtype=torch.float32, device=dev)
+    prior = _dev_f32(block_prior, dev, kd // BLOCK_K, "block_prior", exact=True)
+    # the reference reads block_score_scale[:d_eff] (RRD:104): one entry per scored channel
+    scale = _dev_f32(channel_scale, dev, (kd // BLOCK_K) * BLOCK_K, "channel_scale")
+    opts = _lib.SelectOpts(_SCORES[score], float(energy_keep), prior.data_ptr() if prior is not None else None,
+                           float(prior_alpha), float(prior_eps), scale.data_ptr() if scale is not None else None,
+                           ratio_out.data_ptr() if want_ratio else None)
+    return opts, ratio_out, (prior, scale)
+
+
 def select_topk(x: torch.Tensor, k: int, score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
                 prior_alpha: float = 1.0, prior_eps: float = 0.1, channel_scale: Optional[torch.Tensor] = None,
                 energy_keep: float = 0.0, idx_out: Optional[torch.Tensor] = None,
@@ -107,21 +134,14 @@ def select_topk(x: torch.Tensor, k: int, score: str = "l2_mean", block_prior: Op
         raise ValueError(f"K={kd} has no whole 64-channel block")
     if score not in _SCORES:
         raise ValueError(f"score must be one of {sorted(_SCORES)}")
-    cap = nb if energy_keep > 0 else max(0, min(int(k), nb))
-    if score == "l1":
-        cap = max(0, min(int(k), (kd + BLOCK_K - 1) // BLOCK_K))
+    cap = _capacity(score, k, kd, energy_keep)
     if idx_out is None:
         idx_out = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
     if count_out is None:
         count_out = torch.empty(1, dtype=torch.int32, device=dev)
-    want_ratio = ratio_out is not None or (score != "l1" and energy_keep > 0)
-    if want_ratio and ratio_out is None:
-        ratio_out = torch.empty(1, dtype=torch.float32, device=dev)
-    prior = _dev_f32(block_prior, dev, nb, "block_prior", exact=True)
-    scale = _dev_f32(channel_scale, dev, kd, "channel_scale")
-    opts = _lib.SelectOpts(_SCORES[score], float(energy_keep), prior.data_ptr() if prior is not None else None,
-                           float(prior_alpha), float(prior_eps), scale.data_ptr() if scale is not None else None,
-                           ratio_out.data_ptr() if want_ratio else None)
+    opts, ratio_out, _keep = _rule_opts(dev, kd, score, block_prior, prior_alpha, prior_eps, channel_scale,
+                                        energy_keep, ratio_out)
+    want_ratio = ratio_out is not None
     ws_bytes = int(lib.bsg_select_workspace_bytes(kd))
     ws = _workspace(workspace_prefix, dev, ws_bytes)
     with torch.cuda.device(dev):
@@ -190,17 +210,67 @@ def _energy_expanded_active_blocks(x: torch.Tensor, density: float, block_k: int
 
 def select_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, k: int, cache_prefix: str = "sel_gemm",
                        plan=None, idx_out: Optional[torch.Tensor] = None,
-                       count_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                       count_out: Optional[torch.Tensor] = None, score: str = "l1", **rule) -> Tuple[torch.Tensor, torch.Tensor]:
     """Fused online selection + block-sparse GEMM: out = X[:, top-k blocks] · W[top-k blocks].
 
-    x [B, S, K], weight nn.Linear [N, K], out [B, S, N].  Two launches on the current stream,
-    no host round trip; returns the (device) selected list and count."""
+    x [B, S, K], weight nn.Linear [N, K], out [B, S, N].  score "l1" is the exact-L1 rule
+    (select_gemm_packed); "l2_mean" or "energy" the reference's rules (select_gemm_rule_packed,
+    which takes the options of `rule`: block_prior, prior_alpha, prior_eps, channel_scale,
+    energy_keep, ratio_out).  One to three launches on the current stream, no host round trip;
+    returns the (device) selected list and count."""
     n_dim = out.shape[-1]
     x2d, y2d, bt, m_dim = _views(x, out, n_dim)
     _check_shapes(x2d, weight, y2d, n_dim, m_dim)
     entry = _packed_entry(weight, BLOCK_K, cache_prefix)
-    return select_gemm_packed(x2d, entry.packed, n_dim, k, y2d, plan=plan, idx_out=idx_out, count_out=count_out,
-                              workspace_prefix=f"{cache_prefix}_ws")
+    if score == "l1" and not rule:
+        return select_gemm_packed(x2d, entry.packed, n_dim, k, y2d, plan=plan, idx_out=idx_out, count_out=count_out,
+                                  workspace_prefix=f"{cache_prefix}_ws")
+    idx, cnt, _ = select_gemm_rule_packed(x2d, entry.packed, n_dim, k, y2d, score=score, plan=plan, idx_out=idx_out,
+                                          count_out=count_out, workspace_prefix=f"{cache_prefix}_ws", **rule)
+    return idx, cnt
+
+
+def select_gemm_rule_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor,
+                            score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
+                            prior_alpha: float = 1.0, prior_eps: float = 0.1,
+                            channel_scale: Optional[torch.Tensor] = None, energy_keep: float = 0.0, plan=None,
+                            idx_out: Optional[torch.Tensor] = None, count_out: Optional[torch.Tensor] = None,
+                            ratio_out: Optional[torch.Tensor] = None, workspace_prefix: str = "sel_rule_ws"
+                            ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Selection by the reference's rules (select_topk's options, RRD:90-176) + the GEMM on the
+    kept blocks, one library call (bsg_select_gemm_rule): the kept ids, count and ratio are those
+    select_topk gives for the same x and options, all on the device.  Two launches when the GEMM
+    ranks the fp64 score keys itself (no energy budget, no ratio, fp16), else three.  Returns
+    (idx int32 with room for the capacity, count [1], ratio [1] or None)."""
+    lib = load()
+    dev = _require_cuda(x2d, packed, y2d)
+    bt, m_dim = x2d.shape
+    if m_dim % 8 != 0 or x2d.stride(1) != 1 or x2d.stride(0) % 8 != 0:
+        raise ValueError(f"x must be [bt, K] with unit column stride and K % 8 == 0 (K={m_dim})")
+    nblk = int(packed.shape[0])
+    if (m_dim + BLOCK_K - 1) // BLOCK_K != nblk:
+        raise ValueError(f"x has K={m_dim} but the packed weight has {nblk} K-blocks")
+    if m_dim // BLOCK_K < 1:
+        raise ValueError(f"K={m_dim} has no whole 64-channel block")
+    cap = _capacity(score, k, m_dim, energy_keep)
+    if idx_out is None:
+        idx_out = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    if count_out is None:
+        count_out = torch.empty(1, dtype=torch.int32, device=dev)
+    if int(idx_out.numel()) < cap:
+        raise ValueError(f"idx_out holds {idx_out.numel()} ids, the selection may keep {cap}")
+    opts, ratio_out, _keep = _rule_opts(dev, m_dim, score, block_prior, prior_alpha, prior_eps, channel_scale,
+                                        energy_keep, ratio_out)
+    pl = resolve_plan(bt, n_dim, nblk, cap, dev, plan, select=True)
+    sel_bytes = int(lib.bsg_select_workspace_bytes(m_dim))
+    gemm_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
+    ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes, (bt, n_dim) + pl.as_tuple())
+    with torch.cuda.device(dev):
+        check(lib.bsg_select_gemm_rule(x2d.data_ptr(), x2d.stride(0), bt, m_dim, int(k), ctypes_byref(opts),
+                                       packed.data_ptr(), n_dim, idx_out.data_ptr(), count_out.data_ptr(),
+                                       y2d.data_ptr(), y2d.stride(0), _dtype_code(x2d), ws.data_ptr(),
+                                       sel_bytes + gemm_bytes, ctypes_byref(pl), _stream_handle(dev)))
+    return idx_out, count_out, ratio_out
 
 
 def select_gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor, plan=None,

@@ -59,6 +59,9 @@ def load_table(path: str = TABLE_PATH) -> List[dict]:
     _TABLE = entries
     _INDEX = {}
     _MEMO.clear()
+    from .runtime import forget_prepared_calls
+
+    forget_prepared_calls()
     for e in entries:
         _INDEX.setdefault((int(e["N"]), (int(e["K"]) + BLOCK_K - 1) // BLOCK_K), []).append(e)
     return entries

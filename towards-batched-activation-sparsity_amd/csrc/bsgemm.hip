@@ -79,12 +79,14 @@ int hip_fail(hipError_t e, const char* what) {
 // optionally times max(prior_j + eps, 1e-6)^alpha (RRD:106-112).  Blocks are floor(K/64), as
 // there.  Ranking is (score desc, id asc); with an energy budget the kept count grows from k to
 // the first rank whose cumulative (unscaled) energy reaches budget * total (RRD:155-176).
+// Scores are stored as order keys (score_order_key): unsigned 64-bit values in the order of the
+// fp64 scores, so the rank kernel and a GEMM's in-kernel top-k compare them as integers.
 struct SelScoreParams {
   const void* x;
   int64_t ldx;
   const float* prior;
   const float* scale;
-  double* scores;
+  uint64_t* keys;   // ceil(K/64): floor(K/64) scored blocks, a partial last block at key 0
   double* energy;
   int32_t* idx_out;
   int32_t* na_out;
@@ -104,11 +106,30 @@ __device__ __forceinline__ float elem_to_float<__bf16>(uint32_t b) {
   return __builtin_bit_cast(float, b << 16);
 }
 
+// An fp64 score as an unsigned key in the same order: non-negative values keep their bits
+// with the sign bit set, negative ones are complemented; -0 counts as +0 (they compare equal)
+// and every NaN takes the largest key (a NaN score ranks first, as torch.topk ranks NaN above
+// every number).  Every key of a real score is above 0, the key of padding and of a partial
+// last block.
+__device__ __forceinline__ uint64_t score_order_key(double s) {
+  if (s != s) return ~0ull;
+  const uint64_t b = __builtin_bit_cast(uint64_t, s + 0.0);
+  return (b >> 63) ? ~b : (b | (1ull << 63));
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bsg_score_rule_kernel(SelScoreParams p) {
   __shared__ double s_part[3][4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = blockIdx.x;
+  if (j >= p.nb) {
+    // the partial last block (K % 64 != 0) is never scored (RRD:97-99): lowest key, no energy
+    if (tid == 0) {
+      p.keys[j] = 0;
+      p.energy[j] = 0.0;
+    }
+    return;
+  }
 
   // Thread gi: row gi / 8, channels 64j + 8(gi % 8) .. +7; the 8 threads of a row are
   // adjacent lanes, so a row's sum of squares is a 3-step butterfly.
@@ -163,7 +184,7 @@ __global__ __launch_bounds__(256) void bsg_score_rule_kernel(SelScoreParams p) {
       const double pr = (double)p.prior[j] + (double)p.eps;
       sc *= pow(pr > 1e-6 ? pr : 1e-6, (double)p.alpha);
     }
-    p.scores[j] = sc;
+    p.keys[j] = score_order_key(sc);
     p.energy[j] = en;
   }
 }
@@ -181,14 +202,16 @@ __global__ __launch_bounds__(256) void bsg_rank_rule_kernel(SelScoreParams p) {
   __shared__ int s_keep, s_first;
   const int tid = threadIdx.x;
   const int nb = p.nb;
+  // the order keys first (in s_sc's storage), the cumulative energy by rank after the ranking
+  uint64_t* s_key = (uint64_t*)s_sc;
   for (int i = tid; i < nb; i += 256) {
-    s_sc[i] = p.scores[i];
+    s_key[i] = p.keys[i];
     s_en[i] = p.energy[i];
   }
-  pad_scores(s_sc, nb);
+  pad_scores(s_key, nb);
   __syncthreads();
-  // rank of every block; order[rank] = block
-  for (int j = tid; j < nb; j += 256) s_order[rank_of<false>(s_sc, nb, j, s_sc[j])] = j;
+  // rank of every block; order[rank] = block (keys of real scores are above the pads' 0)
+  for (int j = tid; j < nb; j += 256) s_order[rank_of<false>(s_key, nb, j, s_key[j])] = j;
   const int k0 = p.k < nb ? p.k : nb;
   if (tid == 0) {
     s_keep = k0;
@@ -430,13 +453,33 @@ __global__ __launch_bounds__(1024) void bsg_nmask_kernel(const uint8_t* __restri
 const TileTable* const kTables[] = {&kTilesK1R16, &kTilesK1R32, &kTilesK1R64, &kTilesK2, &kTilesK4, &kTilesK3,
                                     &kTilesK5};
 
-const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
+const KernelEntry* find_kernel_scan(int kind, int rows, int nsub, int wpg, int depth) {
   for (const TileTable* t : kTables)
     for (int i = 0; i < t->n; ++i) {
       const KernelEntry& e = t->e[i];
       if (e.kind == kind && e.rows == rows && e.nsub == nsub && e.wpg == wpg && e.depth == depth) return &e;
     }
   return nullptr;
+}
+
+// A launch looks its tile up two to four times (plan validation, then the launch itself), and
+// eager callers repeat the same few tiles: the last hits of this thread are kept.
+const KernelEntry* find_kernel(int kind, int rows, int nsub, int wpg, int depth) {
+  struct Hit {
+    int kind, rows, nsub, wpg, depth;
+    const KernelEntry* e;
+  };
+  static thread_local Hit hits[4] = {{-1, 0, 0, 0, 0, nullptr}, {-1, 0, 0, 0, 0, nullptr},
+                                     {-1, 0, 0, 0, 0, nullptr}, {-1, 0, 0, 0, 0, nullptr}};
+  static thread_local int next = 0;
+  for (const Hit& h : hits)
+    if (h.kind == kind && h.rows == rows && h.nsub == nsub && h.wpg == wpg && h.depth == depth) return h.e;
+  const KernelEntry* e = find_kernel_scan(kind, rows, nsub, wpg, depth);
+  if (e != nullptr) {
+    hits[next] = Hit{kind, rows, nsub, wpg, depth, e};
+    next = (next + 1) & 3;
+  }
+  return e;
 }
 
 // Kind 3: each wave stages its slice of the list's activation blocks (at most ceil(na / wpg)
@@ -682,6 +725,9 @@ uint64_t* timeline_slot(int64_t) { return nullptr; }
 // count <= nn), and whether Y is compact ([bt, nn * 64], the blocks side by side).
 struct LaunchExtras {
   const uint64_t* scores = nullptr;
+  // the scores are exact-L1 integers below 2^53 (so (score << 11) | id is a unique key); 0 for
+  // any other order key, e.g. the reference rules' (two compares per pair)
+  int score_keyed = 1;
   int32_t* idx_out = nullptr;
   int32_t* na_out = nullptr;
   const int32_t* nidx = nullptr;
@@ -801,7 +847,7 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
   p.scores = ex.scores;
   p.idx_out = ex.idx_out;
   p.na_out = ex.na_out;
-  p.keyed = bt <= 64;
+  p.keyed = ex.score_keyed && bt <= 64;
   p.sort_list = mode == MODE_LIST && ex.sort_list && ex.nidx == nullptr;
   p.nidx = ex.nidx;
   p.nn_dev = ex.nn_dev;
@@ -855,8 +901,17 @@ int noalloc_scratch(char** out, void* stream) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* ptr = nullptr;
+    // The first call may come while this thread's stream is being captured: the symbol lookup is
+    // not a stream operation, so it runs under the relaxed capture mode (the global mode may
+    // refuse it), and the counter clear below then becomes a node of the graph (run on every
+    // replay, before the call's own kernels).
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    e = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess) return hip_fail(e, "hipThreadExchangeStreamCaptureMode");
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t restore = hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (restore != hipSuccess) return hip_fail(restore, "hipThreadExchangeStreamCaptureMode (restore)");
     if (ptr == nullptr || ((uintptr_t)ptr & 255u) != 0) return fail(BSG_ERR_HIP, "scratch address %p", ptr);
     const int64_t n = kScratchCntBytes / 4;
     hipLaunchKernelGGL(bsg_zero_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream,
@@ -1068,21 +1123,21 @@ int bsg_select_topk_l1(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_
   return select_l1_launch(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream, true);
 }
 
-int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
-                    int32_t* idx_out, int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
-  const bsg_select_opts o = opts ? *opts : bsg_select_opts{BSG_SCORE_L1, 0.f, nullptr, 1.f, 0.1f, nullptr, nullptr};
-  if (o.score == BSG_SCORE_L1) {
-    if (o.energy_keep != 0.f || o.block_prior || o.channel_scale || o.ratio_out)
-      return fail(BSG_ERR_UNSUPPORTED, "select: the exact L1 score takes no prior, scale or energy budget");
-    return bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
-  }
+}  // extern "C"
+
+namespace {
+
+const bsg_select_opts kSelectDefaults = {BSG_SCORE_L1, 0.f, nullptr, 1.f, 0.1f, nullptr, nullptr};
+
+// Checks of a reference-rule selection (bsg_select_topk's arguments, score L2 mean or energy).
+int select_rule_check(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts& o,
+                      int32_t* idx_out, int32_t* na_out, int dtype) {
   if (o.score != BSG_SCORE_L2_MEAN && o.score != BSG_SCORE_ENERGY)
     return fail(BSG_ERR_UNSUPPORTED, "select: score=%d (0 = L1, 1 = L2 mean, 2 = energy)", o.score);
   if (dtype != BSG_F16 && dtype != BSG_BF16) return fail(BSG_ERR_DTYPE, "select: dtype=%d", dtype);
   if (bt <= 0 || K < BSG_BLOCK_K)
     return fail(BSG_ERR_ARG, "select: bt=%lld K=%lld (scored blocks are floor(K/64) >= 1)", (long long)bt,
                 (long long)K);
-  const int64_t nb = K / BSG_BLOCK_K;
   if (cdiv(K, BSG_BLOCK_K) > BSG_MAX_NBLK) return fail(BSG_ERR_UNSUPPORTED, "select: K=%lld too large", (long long)K);
   if (k < 0) return fail(BSG_ERR_ARG, "select: k=%d", k);
   if (!(o.energy_keep >= 0.f && o.energy_keep <= 1.f))
@@ -1093,17 +1148,21 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
   if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || !aligned16(x))
     return fail(BSG_ERR_ALIGN, "select: x must be 16-byte aligned, K %% 8 == 0, ldx %% 8 == 0");
   if (bt > (1 << 24)) return fail(BSG_ERR_UNSUPPORTED, "select: bt too large");
-  const int64_t need = bsg_select_workspace_bytes(K);
-  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
-    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
-                (long long)need);
+  return BSG_OK;
+}
+
+// Launches of a checked reference-rule selection: the score launch (order keys and energies of
+// the ceil(K/64) blocks into the selector workspace sel_ws), then, when `rank`, the one-work-group
+// rank launch (ids, count and ratio on the device).
+int select_rule_run(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts& o,
+                    int32_t* idx_out, int32_t* na_out, int dtype, void* sel_ws, void* stream, bool rank) {
   SelScoreParams p;
   p.x = x;
   p.ldx = ldx;
   p.prior = o.block_prior;
   p.scale = o.channel_scale;
-  p.scores = (double*)((char*)ws + 256);
-  p.energy = p.scores + cdiv(K, BSG_BLOCK_K);
+  p.keys = (uint64_t*)((char*)sel_ws + 256);
+  p.energy = (double*)(p.keys + cdiv(K, BSG_BLOCK_K));
   p.idx_out = idx_out;
   p.na_out = na_out;
   p.ratio_out = o.ratio_out;
@@ -1112,19 +1171,42 @@ int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
   p.energy_keep = o.energy_keep;
   p.bt = (int32_t)bt;
   p.K = (int32_t)K;
-  p.nb = (int32_t)nb;
+  p.nb = (int32_t)(K / BSG_BLOCK_K);
   p.k = k;
   p.mode = o.score;
+  const dim3 grid((unsigned)cdiv(K, BSG_BLOCK_K));
   if (dtype == BSG_F16)
-    hipLaunchKernelGGL(bsg_score_rule_kernel<_Float16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(bsg_score_rule_kernel<_Float16>, grid, dim3(256), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL(bsg_score_rule_kernel<__bf16>, dim3((unsigned)nb), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(bsg_score_rule_kernel<__bf16>, grid, dim3(256), 0, (hipStream_t)stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk score launch");
+  if (e != hipSuccess) return hip_fail(e, "reference-rule score launch");
+  if (!rank) return BSG_OK;
   hipLaunchKernelGGL(bsg_rank_rule_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
   e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "bsg_select_topk rank launch");
+  if (e != hipSuccess) return hip_fail(e, "reference-rule rank launch");
   return BSG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bsg_select_topk(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
+                    int32_t* idx_out, int32_t* na_out, int dtype, void* ws, int64_t ws_bytes, void* stream) {
+  const bsg_select_opts o = opts ? *opts : kSelectDefaults;
+  if (o.score == BSG_SCORE_L1) {
+    if (o.energy_keep != 0.f || o.block_prior || o.channel_scale || o.ratio_out)
+      return fail(BSG_ERR_UNSUPPORTED, "select: the exact L1 score takes no prior, scale or energy budget");
+    return bsg_select_topk_l1(x, ldx, bt, K, k, idx_out, na_out, dtype, ws, ws_bytes, stream);
+  }
+  int rc = select_rule_check(x, ldx, bt, K, k, o, idx_out, na_out, dtype);
+  if (rc != BSG_OK) return rc;
+  const int64_t need = bsg_select_workspace_bytes(K);
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select: workspace %lld bytes < %lld (8-byte aligned)", (long long)ws_bytes,
+                (long long)need);
+  return select_rule_run(x, ldx, bt, K, k, o, idx_out, na_out, dtype, ws, stream, true);
 }
 
 int bsg_read_calibrate(const void* src, int64_t bytes, void* sink, void* stream) {
@@ -1224,6 +1306,61 @@ int bsg_select_gemm(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k
                 (long long)ws_bytes, (long long)sel);
   return select_gemm_run(x, ldx, bt, K, k, wp, N, idx_out, na_out, y, ldy, dtype, (uint64_t*)((char*)ws + 256),
                          (char*)ws + sel, ws_bytes - sel, LaunchExtras{}, plan, stream);
+}
+
+int bsg_select_gemm_rule(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const bsg_select_opts* opts,
+                         const void* wp, int64_t N, int32_t* idx_out, int32_t* na_out, void* y, int64_t ldy,
+                         int dtype, void* ws, int64_t ws_bytes, const bsg_plan* plan, void* stream) {
+  const bsg_select_opts o = opts ? *opts : kSelectDefaults;
+  if (o.score == BSG_SCORE_L1) {
+    if (o.energy_keep != 0.f || o.block_prior || o.channel_scale || o.ratio_out)
+      return fail(BSG_ERR_UNSUPPORTED, "select_gemm: the exact L1 score takes no prior, scale or energy budget");
+    return bsg_select_gemm(x, ldx, bt, K, k, wp, N, idx_out, na_out, y, ldy, dtype, ws, ws_bytes, plan, stream);
+  }
+  const int64_t sel = bsg_select_workspace_bytes(K);
+  if (sel < 0) return fail(BSG_ERR_ARG, "select_gemm: K=%lld", (long long)K);
+  if (!ws || ws_bytes < sel || ((uintptr_t)ws & 15u) != 0)
+    return fail(BSG_ERR_WORKSPACE, "select_gemm: workspace %lld bytes < the selector's %lld (16-byte aligned)",
+                (long long)ws_bytes, (long long)sel);
+  int rc = select_rule_check(x, ldx, bt, K, k, o, idx_out, na_out, dtype);
+  if (rc != BSG_OK) return rc;
+  if (N <= 0) return fail(BSG_ERR_ARG, "select_gemm: N=%lld", (long long)N);
+  rc = check_common(x, ldx, bt, K, wp, N, y, ldy, dtype, N);
+  if (rc != BSG_OK) return rc;
+  const int64_t nblk = cdiv(K, BSG_BLOCK_K);
+  const int32_t nb = (int32_t)(K / BSG_BLOCK_K);
+  // GEMM list capacity: every scored block may be kept under an energy budget, else min(k, nb)
+  const int32_t cap = o.energy_keep > 0.f ? nb : (k < nb ? k : nb);
+  bsg_plan pl = plan ? *plan : bsg_plan{0, 0, 0, 0, 0, 0};
+  rc = resolve(bt, N, (int32_t)nblk, cap, pl.split_k == 0 ? device_cu_count() : 256, &pl);
+  if (rc != BSG_OK) return rc;
+  void* gws = (char*)ws + sel;
+  const int64_t gws_bytes = ws_bytes - sel;
+  const int64_t need = gemm_ws_bytes(bt, N, &pl);
+  if (need > 0 && (gws_bytes < need || !aligned16(gws)))
+    return fail(BSG_ERR_WORKSPACE, "select_gemm: GEMM workspace %lld bytes < %lld needed (split_k=%d)",
+                (long long)gws_bytes, (long long)need, pl.split_k);
+  // Without an energy budget or a ratio the kept set is the top min(k, nb) by key, which the GEMM's
+  // work-groups rank themselves (as for the L1 rule, same limits); the budget's cumulative-energy
+  // scan runs in the one-work-group rank launch.
+  const int64_t items = cdiv(nblk, 64) * cdiv(nblk, 16);
+  const KernelEntry* ke = find_kernel(pl.kind, pl.rows_per_group, pl.cols_per_wave / 16, pl.waves_per_group, pl.depth);
+  const bool rank_in_gemm = o.energy_keep == 0.f && o.ratio_out == nullptr && dtype == BSG_F16 &&
+                            nblk <= BSG_TOPK_MAX_NBLK && ke != nullptr && ke->f16_sel != nullptr &&
+                            items <= BSG_TOPK_ITEMS_PER_WAVE * (int64_t)pl.waves_per_group;
+  rc = select_rule_run(x, ldx, bt, K, k, o, idx_out, na_out, dtype, ws, stream, !rank_in_gemm);
+  if (rc != BSG_OK) return rc;
+  if (rank_in_gemm) {
+    LaunchExtras ex;
+    ex.scores = (const uint64_t*)((char*)ws + 256);
+    ex.score_keyed = 0;
+    ex.idx_out = idx_out;
+    ex.na_out = na_out;
+    return launch_gemm(MODE_TOPK, x, ldx, bt, K, wp, N, nullptr, cap, nullptr, nullptr, 0, y, ldy, dtype, gws,
+                       gws_bytes, &pl, stream, ex);
+  }
+  return launch_gemm(MODE_LIST, x, ldx, bt, K, wp, N, idx_out, cap, na_out, nullptr, 0, y, ldy, dtype, gws,
+                     gws_bytes, &pl, stream);
 }
 
 int bsg_select_gemm_noalloc(const void* x, int64_t ldx, int64_t bt, int64_t K, int32_t k, const void* wp,
