@@ -183,3 +183,42 @@ def test_mask_reuse_and_step_schedule(dev, model):
         mask, _, _ = orc.select_scored_ref(x0, orc.n_keep(0.5, x0.shape[1] // 64), score="l2_mean")
         assert_close(y.reshape(-1, y.shape[-1]).float().cpu().numpy(), _oracle(x, w, None, fixed=mask),
                      f"reuse {p}")
+
+
+def test_patched_linear_call_site_follows_input_prior_and_weight_updates(dev):
+    """A decode call site of the patched linear resolves its library call once; later calls
+    with new activations, an in-place prior update, an in-place weight update and a different
+    scale tensor must each give the reference's selection and product (oracle, float64 rules)."""
+    bt, k, n, density = 16, 4096, 1024, 0.4
+    rng = np.random.default_rng(41)
+    w = torch.from_numpy(rng.normal(0, 0.02, size=(n, k)).astype(np.float16)).to(dev)
+    prior = torch.from_numpy(rng.uniform(0, 1, size=k // 64).astype(np.float32)).to(dev)
+    cfg = {"best_kern": "naive", "best_K": 1, "best_tile": None}
+    stats = {"calls": 0, "wall_s": 0.0}
+    nk = orc.n_keep(density, k // 64)
+
+    def call(x, scale=None):
+        xt = torch.from_numpy(x).to(dev).view(bt, 1, k)
+        out = patch._sparse_linear(xt, w, density, cfg, "prep_linear", 64, stats, False, None, block_prior=prior,
+                                   prior_alpha=0.7, prior_eps=0.1, block_score_scale=scale)
+        torch.cuda.synchronize()
+        return out.view(bt, n).float().cpu().numpy()
+
+    def want(x, scale=None):
+        ids, _, _ = orc.select_scored_ref(x, nk, "energy" if scale is not None else "l2_mean",
+                                          prior=prior.cpu().numpy(), alpha=0.7, eps=0.1,
+                                          scale=None if scale is None else scale.cpu().numpy())
+        return orc.gemm_ref(x, w.cpu().numpy(), ids)
+
+    for step in range(3):
+        x = rng.normal(0, 1, size=(bt, k)).astype(np.float16)
+        assert_close(call(x), want(x), f"step {step}")
+    prior.copy_(torch.linspace(2.0, 0.0, k // 64, device=dev))
+    x = rng.normal(0, 1, size=(bt, k)).astype(np.float16)
+    assert_close(call(x), want(x), "after an in-place prior update")
+    with torch.no_grad():
+        w.mul_(-1.0)
+    assert_close(call(x), want(x), "after an in-place weight update")
+    scale = torch.from_numpy(rng.uniform(0.5, 2.0, size=k).astype(np.float32)).to(dev)
+    assert_close(call(x, scale), want(x, scale), "with a channel scale")
+    assert stats["calls"] == 6

@@ -29,14 +29,14 @@ from typing import Dict, List, Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from .runtime import (INDEX_BLOCK_META_SIZE, _build_active_k_bitmap, _check_shapes, _get_prepacked_weight_block_major,
+from .runtime import (_FORGET_HOOKS, INDEX_BLOCK_META_SIZE, _build_active_k_bitmap, _check_shapes, _get_prepacked_weight_block_major,
                       _packed_entry, _prepacked_block_sparse_gemm_from_active_blocks,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload,
                       _prepacked_block_sparse_gemm_from_active_blocks_bitmap_preload_splitk,
                       _prepacked_block_sparse_gemm_from_active_blocks_splitk, _views, make_plan,
                       n_keep_for_density)
 from .select import (_energy_expanded_active_blocks, _prior_or_none, _select_active_blocks, _topk_energy_ratio,
-                     select_gemm_rule_packed)
+                     prepare_select_gemm_rule)
 
 PROJS = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"]
 PROJ_TO_SHAPE = {"q_proj": "qkvo", "k_proj": "qkvo", "v_proj": "qkvo", "o_proj": "qkvo",
@@ -134,6 +134,26 @@ def _sparse_linear(x, weight, density: float, cfg: dict, cache_prefix: str, bloc
     return out.reshape(x.shape[0], n_out) if x.dim() == 2 else out
 
 
+class _PreparedLinear:
+    """One decode call site of `_fused_select_linear` resolved once (packed weight, options with
+    device copies of the prior and scale, plan, workspace: select.RuleCall).  A hit re-checks
+    what its key does not pin: the weight's identity, storage and version, the prior's and the
+    scale's versions, x's alignment and the current device."""
+
+    __slots__ = ("call", "wref", "wptr", "wver", "prior", "prior_ver", "scale", "scale_ver", "dev_index")
+
+    def valid(self, x3, weight, block_prior, block_score_scale) -> bool:
+        return (self.wref() is weight and weight._version == self.wver and weight.data_ptr() == self.wptr
+                and block_prior is self.prior and (block_prior is None or block_prior._version == self.prior_ver)
+                and block_score_scale is self.scale
+                and (block_score_scale is None or block_score_scale._version == self.scale_ver)
+                and x3.data_ptr() % 16 == 0 and torch._C._cuda_getDevice() == self.dev_index)
+
+
+_PREPARED_LINEAR: Dict[tuple, _PreparedLinear] = {}
+_FORGET_HOOKS.append(_PREPARED_LINEAR.clear)
+
+
 def _fused_select_linear(x3, weight, out, density: float, cfg: dict, cache_prefix: str, block_k: int,
                          block_prior, prior_alpha: float, prior_eps: float, block_score_scale) -> None:
     """The reference's selection (`_select_active_blocks`, RRD:90-113: mean L2 norm, or the
@@ -141,7 +161,17 @@ def _fused_select_linear(x3, weight, out, density: float, cfg: dict, cache_prefi
     n_keep = max(1, min(nblk, round(density * nblk)))) and the GEMM on the kept blocks, as one
     library call on the packed weight of `cache_prefix` (the select -> bitmap -> GEMM of
     RRD:207-276 without the host-side steps between them).  The lookup row's split-K and tile
-    become the plan; a naive row without split-K takes the tuned table's plan."""
+    become the plan; a naive row without split-K takes the tuned table's plan.  A repeated call
+    site (same weight, x shape, density, lookup row, prior and scale) reuses its resolved call."""
+    key = (cache_prefix, id(weight), x3.shape, x3.stride(), x3.dtype, x3.get_device(), float(density),
+           str(cfg.get("best_kern")), cfg.get("best_K"), tuple(cfg.get("best_tile") or ()), id(block_prior),
+           id(block_score_scale), float(prior_alpha), float(prior_eps), int(block_k))
+    pc = _PREPARED_LINEAR.get(key)
+    if pc is not None and out.is_contiguous():
+        if pc.valid(x3, weight, block_prior, block_score_scale):
+            pc.call.launch(x3.data_ptr(), out.data_ptr(), torch._C._cuda_getCurrentRawStream(pc.dev_index))
+            return
+        del _PREPARED_LINEAR[key]
     if int(block_k) != INDEX_BLOCK_META_SIZE:
         raise ValueError(f"block_k must be {INDEX_BLOCK_META_SIZE}")
     n_out = out.shape[-1]
@@ -155,11 +185,27 @@ def _fused_select_linear(x3, weight, out, density: float, cfg: dict, cache_prefi
         if not any(plan.as_tuple()):
             plan = None
     entry = _packed_entry(weight, block_k, cache_prefix)
-    select_gemm_rule_packed(x2d, entry.packed, n_out, n_keep_for_density(density, d_in // block_k), y2d,
-                            score="energy" if block_score_scale is not None else "l2_mean",
-                            block_prior=_prior_or_none(block_prior, x2d), prior_alpha=prior_alpha,
-                            prior_eps=prior_eps, channel_scale=block_score_scale, plan=plan,
-                            workspace_prefix=f"{cache_prefix}_selrule_ws")
+    call = prepare_select_gemm_rule(x2d, entry.packed, n_out, n_keep_for_density(density, d_in // block_k), y2d,
+                                    score="energy" if block_score_scale is not None else "l2_mean",
+                                    block_prior=_prior_or_none(block_prior, x2d), prior_alpha=prior_alpha,
+                                    prior_eps=prior_eps, channel_scale=block_score_scale, plan=plan,
+                                    workspace_prefix=f"{cache_prefix}_selrule_ws")
+    dev = x2d.device
+    with torch.cuda.device(dev):
+        call.launch(x2d.data_ptr(), y2d.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    if x2d.data_ptr() == x3.data_ptr() and x3.is_contiguous() and not torch.cuda.is_current_stream_capturing():
+        pc = _PreparedLinear()
+        pc.call = call
+        pc.wref = entry.ref
+        pc.wptr = int(weight.data_ptr())
+        pc.wver = entry.version
+        pc.prior, pc.scale = block_prior, block_score_scale
+        pc.prior_ver = block_prior._version if block_prior is not None else 0
+        pc.scale_ver = block_score_scale._version if block_score_scale is not None else 0
+        pc.dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
+        if len(_PREPARED_LINEAR) >= 4096:
+            _PREPARED_LINEAR.clear()
+        _PREPARED_LINEAR[key] = pc
 
 
 class _SparseForward:

@@ -172,6 +172,8 @@ def release_prepacked_weights(cache_prefix: Optional[str] = None) -> None:
             cache.clear()
     for key in [k for k in _PREPARED if cache_prefix is None or k[0] == cache_prefix]:
         del _PREPARED[key]
+    for hook in _FORGET_HOOKS:
+        hook()
 
 
 # ---------------------------------------------------------------------------------------
@@ -496,9 +498,16 @@ _PREPARED: Dict[tuple, _PreparedCall] = {}
 _PREPARED_MAX = 4096
 
 
+# Other prepared-call caches (the model patch's) register their clear here.
+_FORGET_HOOKS: list = []
+
+
 def forget_prepared_calls() -> None:
-    """Drop every prepared drop-in call (their plans came from tuning state that is being reset)."""
+    """Drop every prepared call (their plans came from tuning state that is being reset, or hold
+    packed weights that are being released)."""
     _PREPARED.clear()
+    for hook in _FORGET_HOOKS:
+        hook()
 
 
 def _prepared_key(x, weight, active_blocks, out, cache_prefix, sort_active_blocks, active_blocks_limit) -> tuple:

@@ -230,18 +230,31 @@ def select_sparse_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
     return idx, cnt
 
 
-def select_gemm_rule_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor,
-                            score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
-                            prior_alpha: float = 1.0, prior_eps: float = 0.1,
-                            channel_scale: Optional[torch.Tensor] = None, energy_keep: float = 0.0, plan=None,
-                            idx_out: Optional[torch.Tensor] = None, count_out: Optional[torch.Tensor] = None,
-                            ratio_out: Optional[torch.Tensor] = None, workspace_prefix: str = "sel_rule_ws"
-                            ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """Selection by the reference's rules (select_topk's options, RRD:90-176) + the GEMM on the
-    kept blocks, one library call (bsg_select_gemm_rule): the kept ids, count and ratio are those
-    select_topk gives for the same x and options, all on the device.  Two launches when the GEMM
-    ranks the fp64 score keys itself (no energy budget, no ratio, fp16), else three.  Returns
-    (idx int32 with room for the capacity, count [1], ratio [1] or None)."""
+class RuleCall:
+    """A select_gemm_rule_packed call resolved once: the bsg_select_opts with device copies of the
+    prior and the channel scale, the plan, the workspace and the id / count / ratio outputs, kept
+    alive with the object; launch(x_ptr, y_ptr, stream) then makes the one library call.  Valid
+    for x of the same shape and strides (row stride ldx), the same packed weight, and prior and
+    scale of unchanged values."""
+
+    __slots__ = ("fn", "bt", "kd", "ldx", "k", "n", "ldy", "code", "wp", "opts", "opts_ref", "plan", "plan_ref",
+                 "ws", "ws_bytes", "idx", "cnt", "ratio", "keep")
+
+    def launch(self, x_ptr: int, y_ptr: int, stream: int) -> None:
+        rc = self.fn(x_ptr, self.ldx, self.bt, self.kd, self.k, self.opts_ref, self.wp, self.n, self.idx.data_ptr(),
+                     self.cnt.data_ptr(), y_ptr, self.ldy, self.code, self.ws, self.ws_bytes, self.plan_ref, stream)
+        if rc != _lib.BSG_OK:
+            check(rc)
+
+
+def prepare_select_gemm_rule(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor,
+                             score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
+                             prior_alpha: float = 1.0, prior_eps: float = 0.1,
+                             channel_scale: Optional[torch.Tensor] = None, energy_keep: float = 0.0, plan=None,
+                             idx_out: Optional[torch.Tensor] = None, count_out: Optional[torch.Tensor] = None,
+                             ratio_out: Optional[torch.Tensor] = None,
+                             workspace_prefix: str = "sel_rule_ws") -> RuleCall:
+    """Checks and resolves a select_gemm_rule_packed call (see there) without launching it."""
     lib = load()
     dev = _require_cuda(x2d, packed, y2d)
     bt, m_dim = x2d.shape
@@ -259,18 +272,44 @@ def select_gemm_rule_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int,
         count_out = torch.empty(1, dtype=torch.int32, device=dev)
     if int(idx_out.numel()) < cap:
         raise ValueError(f"idx_out holds {idx_out.numel()} ids, the selection may keep {cap}")
-    opts, ratio_out, _keep = _rule_opts(dev, m_dim, score, block_prior, prior_alpha, prior_eps, channel_scale,
-                                        energy_keep, ratio_out)
+    opts, ratio_out, keep = _rule_opts(dev, m_dim, score, block_prior, prior_alpha, prior_eps, channel_scale,
+                                       energy_keep, ratio_out)
     pl = resolve_plan(bt, n_dim, nblk, cap, dev, plan, select=True)
     sel_bytes = int(lib.bsg_select_workspace_bytes(m_dim))
     gemm_bytes = int(lib.bsg_gemm_workspace_bytes(bt, n_dim, ctypes_byref(pl)))
     ws = _workspace(workspace_prefix, dev, sel_bytes + gemm_bytes, (bt, n_dim) + pl.as_tuple())
+    c = RuleCall()
+    c.fn = lib.bsg_select_gemm_rule
+    c.bt, c.kd, c.ldx, c.k = int(bt), int(m_dim), int(x2d.stride(0)), int(k)
+    c.n, c.ldy, c.code, c.wp = int(n_dim), int(y2d.stride(0)), _dtype_code(x2d), int(packed.data_ptr())
+    c.opts = opts
+    c.opts_ref = ctypes_byref(opts)
+    c.plan = pl
+    c.plan_ref = ctypes_byref(pl)
+    c.ws, c.ws_bytes = ws.data_ptr(), sel_bytes + gemm_bytes
+    c.idx, c.cnt, c.ratio = idx_out, count_out, ratio_out
+    c.keep = (keep, ws, packed)
+    return c
+
+
+def select_gemm_rule_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor,
+                            score: str = "l2_mean", block_prior: Optional[torch.Tensor] = None,
+                            prior_alpha: float = 1.0, prior_eps: float = 0.1,
+                            channel_scale: Optional[torch.Tensor] = None, energy_keep: float = 0.0, plan=None,
+                            idx_out: Optional[torch.Tensor] = None, count_out: Optional[torch.Tensor] = None,
+                            ratio_out: Optional[torch.Tensor] = None, workspace_prefix: str = "sel_rule_ws"
+                            ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Selection by the reference's rules (select_topk's options, RRD:90-176) + the GEMM on the
+    kept blocks, one library call (bsg_select_gemm_rule): the kept ids, count and ratio are those
+    select_topk gives for the same x and options, all on the device.  Two launches when the GEMM
+    ranks the fp64 score keys itself (no energy budget, no ratio, fp16), else three.  Returns
+    (idx int32 with room for the capacity, count [1], ratio [1] or None)."""
+    c = prepare_select_gemm_rule(x2d, packed, n_dim, k, y2d, score, block_prior, prior_alpha, prior_eps,
+                                 channel_scale, energy_keep, plan, idx_out, count_out, ratio_out, workspace_prefix)
+    dev = x2d.device
     with torch.cuda.device(dev):
-        check(lib.bsg_select_gemm_rule(x2d.data_ptr(), x2d.stride(0), bt, m_dim, int(k), ctypes_byref(opts),
-                                       packed.data_ptr(), n_dim, idx_out.data_ptr(), count_out.data_ptr(),
-                                       y2d.data_ptr(), y2d.stride(0), _dtype_code(x2d), ws.data_ptr(),
-                                       sel_bytes + gemm_bytes, ctypes_byref(pl), _stream_handle(dev)))
-    return idx_out, count_out, ratio_out
+        c.launch(x2d.data_ptr(), y2d.data_ptr(), _stream_handle(dev))
+    return c.idx, c.cnt, c.ratio
 
 
 def select_gemm_packed(x2d: torch.Tensor, packed: torch.Tensor, n_dim: int, k: int, y2d: torch.Tensor, plan=None,
