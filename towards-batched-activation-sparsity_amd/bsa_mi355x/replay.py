@@ -90,8 +90,8 @@ def cases_for_batches(fx: Dict[str, np.ndarray], batches: Sequence[int], steps_p
 
 
 class StepGraphs:
-    """The 224-GEMM decode step of one group-step's map as one hipGraph (SURVEY's oracle-map
-    replay "in one hipGraph"): 32 layers x the 7 projections in the reference's order (q, k, v,
+    """The 224-GEMM decode step of one group-step's map as one hipGraph (the oracle-map replay
+    as a whole step rather than per case): 32 layers x the 7 projections in the reference's order (q, k, v,
     o, gate, up, down; BPS:122-141), each layer with its own random-init weights (the Llama-2-7B
     step's ~13 GB, more than the 256 MB Infinity Cache can hold, so no rotation is needed), each
     GEMM with floor(density * nblk) random active blocks from the map entry (BPS:84-87).  The
