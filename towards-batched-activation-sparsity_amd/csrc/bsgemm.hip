@@ -117,6 +117,24 @@ __device__ __forceinline__ uint64_t score_order_key(double s) {
   return (b >> 63) ? ~b : (b | (1ull << 63));
 }
 
+// x plus lane i - n's x within the same 16-lane row (0 outside it), in fp64.
+template <int CTRL>
+__device__ __forceinline__ double f64_row_shr(double x) {
+  return x + __builtin_bit_cast(double, u64_row_shr<CTRL>(__builtin_bit_cast(uint64_t, x)));
+}
+
+// Sum of lanes 15, 31, 47 and 63 (each row's last lane), the same value in every lane.
+__device__ __forceinline__ double f64_rows_total(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const int lo = (int)(uint32_t)b, hi = (int)(uint32_t)(b >> 32);
+  double r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = __builtin_bit_cast(double, ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, 16 * i + 15) << 32) |
+                                          (uint32_t)__builtin_amdgcn_readlane(lo, 16 * i + 15));
+  return ((r[0] + r[1]) + r[2]) + r[3];
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bsg_score_rule_kernel(SelScoreParams p) {
   __shared__ double s_part[3][4];
@@ -132,42 +150,61 @@ __global__ __launch_bounds__(256) void bsg_score_rule_kernel(SelScoreParams p) {
   }
 
   // Thread gi: row gi / 8, channels 64j + 8(gi % 8) .. +7; the 8 threads of a row are
-  // adjacent lanes, so a row's sum of squares is a 3-step butterfly.
+  // adjacent lanes, so a row's sum of squares is a 3-step butterfly.  The channel scales are
+  // read once, and the 16-byte loads of up to U 32-row groups are in flight before any is
+  // summed, so up to 32 * U rows cost one memory round trip (rows are still summed in order).
+  constexpr int U = 4;
   double a_l2 = 0.0, a_e = 0.0, a_es = 0.0;
   const int rows = p.bt;
-  for (int r0 = 0; r0 < rows; r0 += 32) {
-    const int row = r0 + (tid >> 3);
-    const int c0 = 64 * j + 8 * (tid & 7);
-    double sq = 0.0, sqs = 0.0;
-    if (row < rows) {
-      const u32x4 v = *(const u32x4*)((const uint16_t*)p.x + (size_t)row * (size_t)p.ldx + c0);
-      const uint32_t h[8] = {v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16,
-                             v.z & 0xffffu, v.z >> 16, v.w & 0xffffu, v.w >> 16};
+  const int c0 = 64 * j + 8 * (tid & 7);
+  double scv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const double f = (double)elem_to_float<T>(h[e]);
-        sq += f * f;
-        if (p.scale) sqs += f * f * (double)p.scale[c0 + e];
+  for (int e = 0; e < 8; ++e) scv[e] = p.scale ? (double)p.scale[c0 + e] : 0.0;
+  for (int r0 = 0; r0 < rows; r0 += 32 * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + 32 * u + (tid >> 3);
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (row < rows) v[u] = *(const u32x4*)((const uint16_t*)p.x + (size_t)row * (size_t)p.ldx + c0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + 32 * u + (tid >> 3);
+      double sq = 0.0, sqs = 0.0;
+      if (row < rows) {
+        const uint32_t h[8] = {v[u].x & 0xffffu, v[u].x >> 16, v[u].y & 0xffffu, v[u].y >> 16,
+                               v[u].z & 0xffffu, v[u].z >> 16, v[u].w & 0xffffu, v[u].w >> 16};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const double f = (double)elem_to_float<T>(h[e]);
+          sq += f * f;
+          if (p.scale) sqs += f * f * scv[e];
+        }
+      }
+      // inclusive scans within 16-lane rows (DPP, no LDS round trip): the last lane of each
+      // 8-lane group ends with its row's sum
+      sq = f64_row_shr<0x111>(sq);
+      sq = f64_row_shr<0x112>(sq);
+      sq = f64_row_shr<0x114>(sq);
+      sqs = f64_row_shr<0x111>(sqs);
+      sqs = f64_row_shr<0x112>(sqs);
+      sqs = f64_row_shr<0x114>(sqs);
+      if ((tid & 7) == 7 && row < rows) {
+        a_l2 += sqrt(sq);
+        a_e += sq;
+        a_es += sqs;
       }
     }
-    sq += __shfl_xor(sq, 1, 64);
-    sq += __shfl_xor(sq, 2, 64);
-    sq += __shfl_xor(sq, 4, 64);
-    sqs += __shfl_xor(sqs, 1, 64);
-    sqs += __shfl_xor(sqs, 2, 64);
-    sqs += __shfl_xor(sqs, 4, 64);
-    if ((tid & 7) == 0 && row < rows) {
-      a_l2 += sqrt(sq);
-      a_e += sq;
-      a_es += sqs;
-    }
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    a_l2 += __shfl_xor(a_l2, d, 64);
-    a_e += __shfl_xor(a_e, d, 64);
-    a_es += __shfl_xor(a_es, d, 64);
-  }
+  // lanes 7 and 15 of each row hold the partials: lane 15 takes their sum, and the wave's total
+  // is the four rows' lanes 15, 31, 47 and 63
+  a_l2 = f64_row_shr<0x118>(a_l2);
+  a_e = f64_row_shr<0x118>(a_e);
+  a_es = f64_row_shr<0x118>(a_es);
+  a_l2 = f64_rows_total(a_l2);
+  a_e = f64_rows_total(a_e);
+  a_es = f64_rows_total(a_es);
   if (lane == 0) {
     s_part[0][w] = a_l2;
     s_part[1][w] = a_e;
