@@ -72,7 +72,7 @@ MFMA_PROFILES = {
 }
 # Kernel (symbol prefix) that each plan kind launches.
 KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel",
-                5: "bsg_gemm_vt_kernel", 6: "bsg_gemm_vt_kernel"}
+                5: "bsg_gemm_vt_kernel", 6: "bsg_gemm_vt_kernel", 7: "bsg_gemm_vt_kernel"}
 
 
 def log(msg: str) -> None:

@@ -50,8 +50,8 @@ enum bsg_status {
 /* Launch plan of the GEMM.  A zero field means "choose automatically".
  *   split_k         : work-groups that share one output tile and split the active-block
  *                     list (fp32 partials + in-kernel deterministic reduction), >= 1
- *   cols_per_wave   : output columns per wavefront (kinds 1-4: 16, 32, 64 or 128); kinds 5
- *                     and 6: the most columns one work-group may take (16 x its most subtiles)
+ *   cols_per_wave   : output columns per wavefront (kinds 1-4: 16, 32, 64 or 128); kinds 5-7:
+ *                     the most columns one work-group may take (16 x its most subtiles)
  *   waves_per_group : wavefronts per work-group: 1, 2, 4 or 8
  *   depth           : K-blocks whose loads each wave keeps in flight: 1, 2, 4 or 8
  *   rows_per_group  : batch rows per work-group (16, 32 or 64; 1, 2, 4 or 8 for kind 3); bt
@@ -76,13 +76,17 @@ enum bsg_status {
  *        waves meet in LDS once at the end.  split_k must be 1 (0 resolves to 1).
  *     6  as 5, with the waves splitting the block list only (waves_per_group slices), each
  *        loading both channel halves of its blocks.  split_k must be 1.
- *   Kinds 5 and 6 run 1-D lists only (bsg_gemm_2d rejects them), and only the tiles compiled
- *   into the library resolve (BSG_ERR_UNSUPPORTED names any other); a zero field of a kind 5/6
+ *     7  as 6, with each block's activations loaded into the wave's own LDS slot (16 rows x 64
+ *        contiguous bytes per load) and read back in MFMA order instead of loaded into
+ *        registers; the registers this frees allow four block-slice waves at 64 rows.
+ *        split_k must be 1.
+ *   Kinds 5-7 run 1-D lists only (bsg_gemm_2d rejects them), and only the tiles compiled
+ *   into the library resolve (BSG_ERR_UNSUPPORTED names any other); a zero field of a kind 5-7
  *   plan takes rows 16/32/64 from bt, cols_per_wave 48, waves_per_group 4, depth 4.
  * kind 0 here resolves by heuristic to kind 1 (bt <= 16) or kind 2 (larger bt).  The Python
  * layer does not rely on it: its plans come from a table tuned on the MI355X
- * (bsa_mi355x/tuned_plans.json) whose entries name kinds 1, 2, 4, 5 and 6, or from first-call
- * tuning of problems the table does not hold.
+ * (bsa_mi355x/tuned_plans.json) whose entries name kinds 1, 2, 4, 5, 6 and 7, or from
+ * first-call tuning of problems the table does not hold.
  * Maps onto the reference's Triton tile (BLOCK_B, BLOCK_N, num_warps, num_stages) and
  * split-K factor (shared_mask_batched_triton_min_runtime.py:1296-1299, 1350-1361). */
 typedef struct bsg_plan {

@@ -74,7 +74,13 @@ def test_plan_resolve_rejects():
     assert _resolve(0, 4096, 64, 1)[0] == _lib.BSG_ERR_ARG
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 48, 0, 0, 0, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 24, 0))[0] == _lib.BSG_ERR_UNSUPPORTED
-    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 7))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 8))[0] == _lib.BSG_ERR_UNSUPPORTED
+    # kind 7 (kind 6 with LDS activations): no split-K, and only tiles whose wave reduction fits
+    # the waves' activation slots (at most 2 x depth subtiles) are compiled
+    assert _resolve(64, 4096, 64, 1, plan=_lib.Plan(2, 48, 4, 2, 64, 7))[0] == _lib.BSG_ERR_UNSUPPORTED
+    assert _resolve(64, 4096, 64, 1, plan=_lib.Plan(1, 96, 2, 2, 64, 7))[0] == _lib.BSG_ERR_UNSUPPORTED
+    rc, p = _resolve(64, 4096, 64, 1, plan=_lib.Plan(0, 0, 0, 0, 0, 7))
+    assert rc == 0 and p.as_tuple() == (1, 48, 4, 4, 64, 7)
     # kind 5 (variable-width column groups): no split-K, only its instantiated widths
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(2, 48, 4, 4, 16, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
     assert _resolve(16, 4096, 64, 1, plan=_lib.Plan(1, 80, 4, 4, 16, 5))[0] == _lib.BSG_ERR_UNSUPPORTED
@@ -126,7 +132,7 @@ def test_header_documents_every_plan_kind():
     table names is among them (a C caller reading the header can form any shipped plan)."""
     doc = _plan_doc_kinds()
     accepted = _accepted_kinds() - {0}
-    assert accepted == {1, 2, 3, 4, 5, 6}
+    assert accepted == {1, 2, 3, 4, 5, 6, 7}
     assert set(doc) == accepted, (sorted(doc), sorted(accepted))
     for kind in accepted:
         rows = 4 if kind == 3 else 16

@@ -109,6 +109,48 @@ def test_duplicate_ids_accumulate_twice(dev):
     assert_close(y, ref, "duplicates")
 
 
+@pytest.mark.parametrize("bt,plan", [(64, (1, 48, 4, 2, 64, 7)), (64, (1, 48, 4, 4, 64, 7)),
+                                     (37, (1, 32, 4, 2, 32, 7)), (5, (1, 32, 4, 4, 16, 7))])
+def test_lds_activation_kind_skips_exactly(dev, bt, plan):
+    """Kind 7 loads each block's activations into LDS slots that the next blocks reuse; a slot
+    of a skipped entry (leading pad, out-of-range id) must hold zeros, not what the slot held
+    before.  A launch on an all-Inf activation first leaves Inf in every slot of every compute
+    unit's LDS; then Inf and NaN sit in blocks that are never active, the list repeats one id
+    and names ids outside [0, nblk), and its length leaves pad slots in every wave.  Exactly the
+    oracle's result on the listed blocks (duplicates twice), finite, and bit-identical on a
+    repeat."""
+    k, n = 64 * 40, 1100
+    nblk = orc.nblk_of(k)
+    x, w_nk, _ = case(41 + bt, bt, k, n, 1, "normal")
+    # the poisoned blocks are ordinary ids that are simply not in the list
+    x[:, 64 * 7:64 * 8] = np.inf
+    x[: (bt + 1) // 2, 64 * 23 + 5] = np.nan
+    rng = np.random.default_rng(bt)
+    valid = np.setdiff1d(np.arange(nblk), [7, 23])
+    keep = rng.choice(valid, size=13, replace=False)
+    idx = np.concatenate([keep, [keep[2], -1, nblk, nblk + 40]]).astype(np.int32)
+    rng.shuffle(idx)
+    ref = orc.gemm_ref64(x, w_nk, keep) + orc.gemm_ref64(x, w_nk, [keep[2]])
+    xt, it = to_dev(x, dev), to_dev(idx, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    p = bsa.Plan(*plan)
+    outs = []
+    for _ in range(2):
+        junk = torch.empty((bt, n), dtype=F16, device=dev)
+        bsa.gemm_packed(torch.full_like(xt, float("inf")), packed, n, to_dev(np.arange(nblk, dtype=np.int32), dev),
+                        junk, plan=p, workspace_prefix="k7")
+        out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        print(f"kind 7 plan={plan} bt={bt} poisoned inactive blocks", flush=True)
+        used = bsa.gemm_packed(xt, packed, n, it, out, plan=p, workspace_prefix="k7")
+        assert used.as_tuple() == p.as_tuple(), used
+        torch.cuda.synchronize()
+        outs.append(out)
+    y = outs[0].float().cpu().numpy()
+    assert np.isfinite(y).all()
+    assert_close(y, ref, f"kind 7 {plan} bt={bt}")
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def test_dropin_prepared_call_rechecks_what_its_key_does_not_pin(dev):
     """A repeated drop-in call site takes a prepared launch (packed weight, plan and workspace of
     its first call).  Every change its key does not pin must still be honoured: new x and out
@@ -180,7 +222,7 @@ def test_every_instantiated_tile(dev):
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     packed_b = bsa.pack_weight(wb.to(dev))
     for kind, rows, cols, waves, depth in tiles:
-        for sk in ((1,) if kind in (3, 5, 6) else (1, 3)):
+        for sk in ((1,) if kind in (3, 5, 6, 7) else (1, 3)):
             # explicit plan through gemm_packed, so rows_per_group is honoured even when < bt
             out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
             p = bsa.Plan(sk, cols, waves, depth, rows, kind)
@@ -191,7 +233,7 @@ def test_every_instantiated_tile(dev):
         # bf16 once per tile (split-K 2)
         out_b = torch.full((bt, n), float("nan"), dtype=torch.bfloat16, device=dev)
         bsa.gemm_packed(xb.to(dev), packed_b, n, it, out_b,
-                        plan=bsa.Plan(1 if kind in (3, 5, 6) else 2, cols, waves, depth, rows, kind),
+                        plan=bsa.Plan(1 if kind in (3, 5, 6, 7) else 2, cols, waves, depth, rows, kind),
                         workspace_prefix="tiles_bf")
         torch.cuda.synchronize()
         yb = out_b.float().cpu().numpy()
@@ -521,6 +563,8 @@ def test_strided_rows_and_side_stream(dev, plan):
     (3, (1, 16, 4, 4, 4, 3)),     # kind 3
     (9, (1, 48, 4, 4, 16, 5)),    # kind 5
     (50, (1, 48, 2, 4, 64, 6)),   # kind 6
+    (50, (1, 48, 4, 2, 64, 7)),   # kind 7 (activations through LDS)
+    (20, (1, 32, 4, 4, 32, 7)),
 ])
 def test_pipeline_every_slice_length(dev, bt, plan):
     """Each wave's slice is rounded up to the prefetch depth with leading out-of-range slots and
@@ -533,7 +577,7 @@ def test_pipeline_every_slice_length(dev, bt, plan):
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     p = bsa.Plan(*plan)
     splitters = p.split_k * (p.waves_per_group if p.kind in (1, 3) else 1) * \
-        (p.waves_per_group // 2 if p.kind == 5 else (p.waves_per_group if p.kind == 6 else 1))
+        (p.waves_per_group // 2 if p.kind == 5 else (p.waves_per_group if p.kind in (6, 7) else 1))
     top = min(nblk, 2 * splitters * p.depth + p.depth + 1)
     rng = np.random.default_rng(bt)
     for na in range(0, top + 1):
@@ -559,7 +603,8 @@ def test_variable_width_column_groups(dev, bt, k, n, na):
     packed = bsa.pack_weight(to_dev(w_nk, dev))
     ref = orc.gemm_ref64(x, w_nk, idx)
     rows = 16 if bt <= 16 else (32 if bt <= 32 else 64)
-    k6 = {16: ((6, 48, 2, 4), (6, 48, 4, 4)), 32: ((6, 48, 2, 4), (6, 48, 4, 2)), 64: ((6, 48, 2, 2), (6, 48, 4, 2))}
+    k6 = {16: ((6, 48, 2, 4), (6, 48, 4, 4), (7, 32, 4, 4)), 32: ((6, 48, 2, 4), (6, 48, 4, 2), (7, 48, 4, 2)),
+          64: ((6, 48, 2, 2), (6, 48, 4, 2), (7, 48, 4, 2), (7, 48, 4, 4))}
     for kind, cols, waves, depth in ((5, 48, 4, 4), (5, 32, 2, 4), (5, 96, 2, 4), (5, 16, 4, 4)) + k6[rows]:
         p = bsa.Plan(1, cols, waves, depth, rows, kind)
         out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)

@@ -21,7 +21,7 @@ def test_shipped_table_covers_baseline_shapes():
     assert any(e["dense"] for e in entries)
     lib = bsa.load()
     for e in entries:
-        assert len(e["plan"]) == 6 and e["plan"][0] >= 1 and e["plan"][5] in (1, 2, 3, 4, 5, 6)
+        assert len(e["plan"]) == 6 and e["plan"][0] >= 1 and e["plan"][5] in (1, 2, 3, 4, 5, 6, 7)
         # every shipped plan names an instantiated kernel the library accepts as is
         p = bsa.Plan(*e["plan"])
         want = p.as_tuple()
@@ -274,7 +274,7 @@ def test_bench_default_measures_configs2_with_active_byte_rotation():
         copies = min(need[sh], bench.copies_for(active))
         assert copies * active >= 1 << 30, (name, copies, active)
     assert bench.KERNEL_NAMES[4] == "bsg_gemm_xl_kernel"
-    assert set(bench.KERNEL_NAMES) == {1, 2, 3, 4, 5, 6}
+    assert set(bench.KERNEL_NAMES) == {1, 2, 3, 4, 5, 6, 7}
 
 
 def test_bench_default_line_carries_configs3_configs4_and_the_perstep_table(monkeypatch):

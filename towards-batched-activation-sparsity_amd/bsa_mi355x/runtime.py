@@ -705,7 +705,7 @@ def dense_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, cache_p
 def kernel_tiles() -> Sequence[tuple]:
     """Instantiated (kind, rows_per_group, cols_per_wave, waves_per_group, depth) tuples."""
     out = []
-    for kind in (1, 2, 3, 4, 5, 6):
+    for kind in (1, 2, 3, 4, 5, 6, 7):
         for rows in ((1, 2, 4, 8) if kind == 3 else (16, 32, 64)):
             for cols in ((16, 32, 48, 64, 96) if kind >= 5 else (16, 32, 64, 128)):
                 for waves in (1, 2, 4, 8):

@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG_ROOT, "csrc")
 # The C ABI and host code, then the tile tables (each instantiates a slice of the kernel
 # templates of bsg_device.hpp); the units compile in parallel and link into one library.
 SOURCES = ["bsgemm.hip", "tiles_k1_r16.hip", "tiles_k1_r32.hip", "tiles_k1_r64.hip", "tiles_k2.hip",
-           "tiles_k4.hip", "tiles_k3.hip", "tiles_k5.hip"]
+           "tiles_k4.hip", "tiles_k3.hip", "tiles_k5.hip", "tiles_k7.hip"]
 SRC = os.path.join(CSRC, "bsgemm.hip")
 INCLUDE = os.path.join(REPO_ROOT, "include")
 OUT = os.path.join(PKG_ROOT, "bsa_mi355x", "libbsgemm.so")

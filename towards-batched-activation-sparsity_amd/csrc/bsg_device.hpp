@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "bsgemm.h"
 
@@ -47,7 +48,7 @@ struct GemmParams {
 
 typedef void (*GemmFn)(GemmParams);
 
-enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4, KIND_VT = 5, KIND_VT1 = 6 };
+enum { KIND_KSPLIT = 1, KIND_XLDS = 2, KIND_FMA = 3, KIND_XLDS_KH = 4, KIND_VT = 5, KIND_VT1 = 6, KIND_VT1X = 7 };
 
 // 1-D and, for tiles of at most 64 columns per work-group, 2-D (active output blocks) entries.
 // f16_sel: the fp16 1-D form compiled with the in-GEMM top-k (MODE_TOPK; on 16-row tiles also
@@ -64,7 +65,7 @@ struct TileTable {
   int n;
 };
 
-extern const TileTable kTilesK1R16, kTilesK1R32, kTilesK1R64, kTilesK2, kTilesK4, kTilesK3, kTilesK5;
+extern const TileTable kTilesK1R16, kTilesK1R32, kTilesK1R64, kTilesK2, kTilesK4, kTilesK3, kTilesK5, kTilesK7;
 
 }  // namespace bsgk
 
@@ -151,6 +152,34 @@ __device__ __forceinline__ u32x4 ld16(__amdgpu_buffer_rsrc_t r, int voff) {
 
 __device__ __forceinline__ u32x4 ld16_stream(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, BSG_W_AUX);
+}
+
+// fn(std::integral_constant<int, i>) for i = 0 .. N-1, in order.
+template <typename Fn, int... I>
+__device__ __forceinline__ void static_for_seq(Fn&& fn, std::integer_sequence<int, I...>) {
+  (fn(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& fn) {
+  static_for_seq(fn, std::make_integer_sequence<int, N>{});
+}
+
+// 16 bytes per lane straight into LDS: lane i's bytes land at lds + 16 i (an out-of-range offset
+// writes zeros).  No register receives them, and the compiler's wait insertion does not order
+// later LDS reads after such a load, so its users wait by count (vmem_wait).
+__device__ __forceinline__ void ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding (s_waitcnt vmcnt, gfx9
+// encoding; the expcnt and lgkmcnt fields at their maxima), fenced so that no instruction moves
+// across it.  Loads complete in issue order, so every load issued N or more loads before is done.
+template <int N>
+__device__ __forceinline__ void vmem_wait() {
+  constexpr int n = N < 63 ? N : 63;
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <typename T>
@@ -1254,15 +1283,33 @@ __device__ __forceinline__ void vt_columns(int t, int G, int T, int* first, int*
 // KH = 1 (kind 6): no channel-half split; each of the WB waves loads both halves of every
 // weight subtile and activation row tile of its blocks (the two halves of an activation row are
 // one 128-byte line, requested back to back by one wave).
-template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SEL = false>
+// XL (kind 7, with KH = 1): the activations go through LDS instead of registers.  Each block's
+// BTT*16 rows x 64 channels arrive by 16-byte-per-lane loads straight into the wave's own slot
+// of LDS, 16 rows x 64 contiguous bytes per load (a quad of lanes covers one half row, where the
+// register form requests 16 rows x 16 bytes per quad), and are read back in MFMA order.  The
+// quad's 16-byte chunks are rotated by row / 4 so that those reads hit 16 distinct bank groups
+// per 16 lanes.  The registers the activations no longer hold leave room for four block-slice
+// waves; the wave reduction reuses each wave's own slots.
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SEL = false, bool XL = false>
 __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p) {
   constexpr int NW = KH * WB;
   constexpr int NT = 64 * NW;
   constexpr int F = BTT * NSUB;
   constexpr int HP = 3 - KH;  // halves per wave
+  static_assert(!XL || (KH == 1 && F <= DEPTH * BTT * HP), "kind 7: one wave per block, reduction in its slots");
+  constexpr int XS = XL ? NW * DEPTH * BTT * HP : 1;  // 1 KiB activation slots (kind 7)
+  constexpr int RS = XL ? 1 : NW * F;                  // 1 KiB reduction slots (kinds 5, 6)
   __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
-  __shared__ __attribute__((aligned(16))) f32x4 s_red[NW][F][64];
+  __shared__ __attribute__((aligned(16))) u32x4 s_x[XS][64];
+  __shared__ __attribute__((aligned(16))) f32x4 s_red_own[RS][64];
   __shared__ int s_misc[NW + 2];
+  // fragment f of wave ww's partial accumulators
+  auto s_red = [&](int ww, int f) -> f32x4* {
+    if constexpr (XL)
+      return (f32x4*)&s_x[ww * DEPTH * BTT * HP + f][0];
+    else
+      return &s_red_own[ww * F + f][0];
+  };
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1283,29 +1330,36 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
   const int cnt = pend - pbeg;
 
   const int blk_bytes = p.npad * 128;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  // register activations (kinds 5, 6): lane = row (lane % 16) x 16-byte chunk (lane / 16)
   int xrow_off[BTT];
   bool xrow_ok[BTT];
+  // LDS activations (kind 7): lane 4q + c loads row q, chunk (c + q / 4) % 4 of a half, and
+  // MFMA lane m reads its (row m % 16, chunk m / 16) back at rd_pos
+  const int xq = XL ? lane >> 2 : lane & 15;
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi) {
-    const int row = y0 + 16 * bi + (lane & 15);
+    const int row = y0 + 16 * bi + xq;
     xrow_ok[bi] = row < p.bt;
     xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
   }
-  const int xcol = 32 * h + 8 * (lane >> 4);
+  const int xcol = XL ? 8 * (((lane & 3) + (xq >> 2)) & 3) : 32 * h + 8 * (lane >> 4);
+  const int rd_pos = 4 * (lane & 15) + (((lane >> 4) - ((lane & 15) >> 2)) & 3);
   int woff[NSUB];
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) woff[s] = s < nv ? lane * 16 + (st + s) * 2048 + h * 1024 : kOOB;
 
+  constexpr int XR = XL ? 1 : DEPTH;  // slots of register activations
   u32x4 wv[DEPTH][NSUB][HP];
-  u32x4 xv[DEPTH][BTT][HP];
+  u32x4 xv[XR][BTT][HP];
   f32x4 acc[BTT][NSUB];
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto issue = [&](u32x4 (&wd)[NSUB][HP], u32x4 (&xd)[BTT][HP], int t) {
+  // Slot d's loads for list entry t: kind 7 issues its activation loads (into LDS slot d)
+  // before the weights, so that the weights' waits cover them too.
+  auto issue = [&](int d, int t) {
     const bool in = (unsigned)t < (unsigned)cnt;
     const int q = in ? pbeg + t : 0;
     int blk = s_ids[q];
@@ -1313,31 +1367,63 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
     // A skipped slot reads zeros through an empty resource (as its weights do), so the lanes'
     // selects below do not depend on `ok`: a uniform branch there let the register allocator
     // reuse an in-flight load's register and drain the pipeline (vmcnt(0)) every block.
     const __amdgpu_buffer_rsrc_t xb = make_rsrc(p.x, ok ? p.x_bytes : 0);
     const int col = (ok ? blk : 0) * 64 + xcol;
-#pragma unroll
-    for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh) {
-        const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
-        xd[bi][hh] = ld16(xb, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
-      }
-  };
-
-  auto compute = [&](const u32x4 (&wd)[NSUB][HP], const u32x4 (&xd)[BTT][HP]) {
-#pragma unroll
-    for (int hh = 0; hh < HP; ++hh)
+    if constexpr (XL) {
 #pragma unroll
       for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][hh], xd[bi][hh], acc[bi][s]);
+        for (int hh = 0; hh < HP; ++hh) {
+          const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
+          ld16_lds(xb, &s_x[((w * DEPTH + d) * BTT + bi) * HP + hh][0], v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh) wv[d][s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
+    if constexpr (!XL) {
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int hh = 0; hh < HP; ++hh) {
+          const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
+          xv[d][bi][hh] = ld16(xb, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+        }
+    }
+  };
+
+  auto compute = [&](int d) {
+    if constexpr (XL) {
+      u32x4 xl[BTT][HP];
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int hh = 0; hh < HP; ++hh) xl[bi][hh] = s_x[((w * DEPTH + d) * BTT + bi) * HP + hh][rd_pos];
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh)
+#pragma unroll
+        for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xl[bi][hh], acc[bi][s]);
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh)
+#pragma unroll
+        for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xv[d][bi][hh], acc[bi][s]);
+    }
+  };
+
+  // Kind 7: before slot d's LDS reads, every load up to its weights is done; `later` slots' loads
+  // (one slot = BTT*HP activation + NSUB*HP weight loads) and its own weights may be in flight.
+  constexpr int LX = BTT * HP, LW = NSUB * HP;
+  auto wait_slot = [&](auto later) {
+    if constexpr (XL) vmem_wait<LW + decltype(later)::value * (LX + LW)>();
   };
 
   // Rolling pipeline as in kind 1: leading out-of-range slots, branch-free passes, a drain.
@@ -1345,38 +1431,41 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
     const int U = cnt + pad;
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d - pad);
+    for (int d = 0; d < DEPTH; ++d) issue(d, d - pad);
     int u0 = 0;
     for (; u0 + DEPTH < U; u0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
-        compute(wv[d], xv[d]);
+        wait_slot(std::integral_constant<int, DEPTH - 1>{});
+        compute(d);
         BSG_TL_IF(2, u0 + d == pad);
-        issue(wv[d], xv[d], u0 + d + DEPTH - pad);
+        issue(d, u0 + d + DEPTH - pad);
         // Keep slot d's loads between its MFMAs and slot d+1's: left free, the scheduler may
         // gather a pass's MFMAs above its loads (each pass then waits for every block in
         // flight: vmcnt(0)), and which kernels it does this to changes with unrelated code.
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      compute(wv[d], xv[d]);
+    static_for<DEPTH>([&](auto dd) {
+      constexpr int d = decltype(dd)::value;
+      wait_slot(std::integral_constant<int, DEPTH - 1 - d>{});
+      compute(d);
       BSG_TL_IF(2, u0 + d == pad);
-    }
+    });
   }
   BSG_TL_LOOP_END();
 
-  // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read: s_red is separate).
+  // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read; kind 7 writes its
+  // own slots, whose activation loads have all been waited for and read).
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) s_red[w][bi * NSUB + s][lane] = acc[bi][s];
+    for (int s = 0; s < NSUB; ++s) s_red(w, bi * NSUB + s)[lane] = acc[bi][s];
   __syncthreads();
   for (int f = w; f < F; f += NW) {
-    f32x4 v = s_red[0][f][lane];
+    f32x4 v = s_red(0, f)[lane];
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) v += s_red[ww][f][lane];
+    for (int ww = 1; ww < NW; ++ww) v += s_red(ww, f)[lane];
     if (f % NSUB < nv) store_y<T, NSUB>(p, y0, st * 16, f, v);
   }
   BSG_TL(4);
@@ -1412,8 +1501,10 @@ constexpr GemmFn kernel_sel() {
     return bsg_gemm_xl_kernel<_Float16, B, S, W / 2, 2, D, false, true>;
   } else if constexpr (KIND == KIND_VT) {
     return bsg_gemm_vt_kernel<_Float16, B, S, W / 2, D, 2, true>;
-  } else {
+  } else if constexpr (KIND == KIND_VT1) {
     return bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, true>;
+  } else {
+    return bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, true, true>;
   }
 }
 
@@ -1435,6 +1526,9 @@ constexpr GemmFn kernel_sel() {
 #define BSG_V1(B, S, W, D)                                                                                \
   {KIND_VT1, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1>, bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1>, \
    nullptr, nullptr, kernel_sel<KIND_VT1, B, S, W, D>()}
+#define BSG_V1X(B, S, W, D)                                                                                    \
+  {KIND_VT1X, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, false, true>,                        \
+   bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1, false, true>, nullptr, nullptr, kernel_sel<KIND_VT1X, B, S, W, D>()}
 #define BSG_F(R, S, W, D)                                                                                 \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
    kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>(), nullptr}

@@ -488,7 +488,7 @@ __global__ __launch_bounds__(1024) void bsg_nmask_kernel(const uint8_t* __restri
 
 // The whole instantiated tile set, one table per translation unit.
 const TileTable* const kTables[] = {&kTilesK1R16, &kTilesK1R32, &kTilesK1R64, &kTilesK2, &kTilesK4, &kTilesK3,
-                                    &kTilesK5};
+                                    &kTilesK5, &kTilesK7};
 
 const KernelEntry* find_kernel_scan(int kind, int rows, int nsub, int wpg, int depth) {
   for (const TileTable* t : kTables)
@@ -566,7 +566,7 @@ int resolve_fma(int64_t bt, int32_t na, bsg_plan* pl) {
   return BSG_OK;
 }
 
-// Kind 5 and 6 plans: explicit or tuned only; no split-K (their groups already fill the chip).
+// Kind 5, 6 and 7 plans: explicit or tuned only; no split-K (their groups already fill the chip).
 int resolve_vt(bsg_plan* pl) {
   const int rpg = pl->rows_per_group;
   if (rpg != 16 && rpg != 32 && rpg != 64)
@@ -599,11 +599,12 @@ int resolve(int64_t bt, int64_t N, int32_t nblk, int32_t na, int32_t cu, bsg_pla
   if (bt <= 0 || N <= 0 || nblk <= 0 || na < 0 || cu <= 0)
     return fail(BSG_ERR_ARG, "plan: bt=%lld N=%lld nblk=%d na=%d cu=%d", (long long)bt, (long long)N,
                 nblk, na, cu);
-  if (pl->kind < 0 || pl->kind > KIND_VT1)
+  if (pl->kind < 0 || pl->kind > KIND_VT1X)
     return fail(BSG_ERR_UNSUPPORTED, "plan: kind=%d (1 = waves split the block list, 2 = X tile in LDS, "
                 "3 = fp32 dot products for 1-8 rows, 4 = as 2 with channel-half waves, 5 = variable-width "
-                "column groups, 6 = as 5 with waves splitting blocks only)", pl->kind);
-  if (pl->kind == KIND_VT || pl->kind == KIND_VT1) {
+                "column groups, 6 = as 5 with waves splitting blocks only, 7 = as 6 with the activations "
+                "loaded into LDS)", pl->kind);
+  if (pl->kind == KIND_VT || pl->kind == KIND_VT1 || pl->kind == KIND_VT1X) {
     if (pl->rows_per_group == 0) pl->rows_per_group = bt <= 16 ? 16 : (bt <= 32 ? 32 : 64);
     return resolve_vt(pl);
   }
@@ -848,9 +849,9 @@ int launch_gemm(int mode, const void* x, int64_t ldx, int64_t bt, int64_t K, con
                 "cols_per_wave x column waves)", (long long)gc);
   // 2-D: 64 / gc tiles per active output block (a device-side count leaves tiles idle)
   const int64_t ygroups = cdiv(bt, pl.rows_per_group);
-  const bool vt = pl.kind == KIND_VT || pl.kind == KIND_VT1;
+  const bool vt = pl.kind == KIND_VT || pl.kind == KIND_VT1 || pl.kind == KIND_VT1X;
   if (vt && ex.nidx != nullptr)
-    return fail(BSG_ERR_UNSUPPORTED, "2-D: kinds 5 and 6 (variable-width column groups) have no 2-D form");
+    return fail(BSG_ERR_UNSUPPORTED, "2-D: kinds 5-7 (variable-width column groups) have no 2-D form");
   const int64_t n_tiles = vt ? vt_groups(N, ygroups, device_cu_count(), &pl)
                           : ex.nidx != nullptr ? (int64_t)ex.nn * (64 / gc) : cdiv(npad, gc);
   if (n_tiles * pl.split_k > 0x7fffffff || ygroups > 65535) return fail(BSG_ERR_UNSUPPORTED, "grid too large");
