@@ -63,16 +63,18 @@ X_DIST = {"qkvo": "normal", "gate_up": "normal", "down": "laplace"}
 # Committed PMC summaries (HBM bytes per launch) of the roofline point of each workload.
 TRAFFIC_PROFILES = {
     "down_b16_s500": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_down_b16_s500.md"),
-    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_vt_gate_up_b64_s520.md"),
+    "gate_up_b16_s638": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_vt_gate_up_b16_s638.md"),
+    "gate_up_b64_s520": os.path.join(ROOT, "profiles", "traffic_bsg_gemm_vtx_gate_up_b64_s520.md"),
 }
 # MFMA utilisation from counters (SQ_VALU_MFMA_BUSY_CYCLES) of the roofline point's kernel.
 MFMA_PROFILES = {
     "down_b16_s500": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_down_b16_s500.md"),
+    "gate_up_b16_s638": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_gate_up_b16_s638.md"),
     "gate_up_b64_s520": os.path.join(ROOT, "profiles", "pmc_lds_mfma_bsg_gemm_gate_up_b64_s520.md"),
 }
 # Kernel (symbol prefix) that each plan kind launches.
 KERNEL_NAMES = {1: "bsg_gemm_kernel", 2: "bsg_gemm_xl_kernel", 3: "bsg_gemm_fma_kernel", 4: "bsg_gemm_xl_kernel",
-                5: "bsg_gemm_vt_kernel", 6: "bsg_gemm_vt_kernel", 7: "bsg_gemm_vt_kernel"}
+                5: "bsg_gemm_vt_kernel", 6: "bsg_gemm_vt_kernel", 7: "bsg_gemm_vtx_kernel"}
 
 
 def log(msg: str) -> None:
@@ -645,6 +647,10 @@ def run_matrix(args, dev):
     if not args.only and focus != "down_b16_s500" and any(p.name == "down_b16_s500" for p in points):
         # the CPU-reference configuration beside it
         roofline["cpu_reference_point"] = roofline_of("down_b16_s500", True)
+    big = max((p for p in points if p.in_step and not p.dense), key=lambda p: (p.active_bytes, p.name), default=None)
+    if not args.only and big is not None and big.name != focus:
+        # the matrix's largest sparse launch (configs[3]'s GEMM), whichever kernel runs it
+        roofline["largest_sparse_point"] = roofline_of(big.name, True)
     if not args.only:
         # hipBLASLt (torch.mm, the reference's dense baseline) beside every dense point, so the
         # dense kernel the speedups divide by is shown against the vendor library at each batch

@@ -191,7 +191,8 @@ def test_bench_traffic_profile_per_roofline_point():
     spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(root, "bench.py"))
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    algorithmic = {"down_b16_s500": 86 * 64 * 4096 * 2, "gate_up_b64_s520": 31 * 64 * 11008 * 2}
+    algorithmic = {"down_b16_s500": 86 * 64 * 4096 * 2, "gate_up_b64_s520": 31 * 64 * 11008 * 2,
+                   "gate_up_b16_s638": 23 * 64 * 11008 * 2}
     assert set(bench.TRAFFIC_PROFILES) == set(algorithmic)
     for point, path in bench.TRAFFIC_PROFILES.items():
         assert point.split("_s")[0].replace("_", "") in os.path.basename(path).replace("_", "")
@@ -202,13 +203,14 @@ def test_bench_traffic_profile_per_roofline_point():
 
 def test_bench_roofline_profiles_match_the_tuned_kernel():
     """The committed traffic and counter summaries of the llama roofline points (the dominant
-    kernel's CPU-reference point, down B=16 s=0.5, and the largest sparse point, gate/up B=64
-    s=0.52) were taken on the kernel their tuned plans launch now (a retune that changes the kernel
-    makes them stale)."""
+    kernel's largest sparse launch, gate/up B=16 s=0.638 with the shipped plans; the CPU-reference
+    point, down B=16 s=0.5; the matrix's largest sparse launch, gate/up B=64 s=0.52) were taken on
+    the kernel their tuned plans launch now (a retune that changes the kernel makes them stale)."""
     bench = _bench_module()
     from bsa_mi355x import tuning
 
     for point, (bt, n, nblk, na) in (("gate_up_b64_s520", (64, 11008, 64, 31)),
+                                     ("gate_up_b16_s638", (16, 11008, 64, 23)),
                                      ("down_b16_s500", (16, 4096, 172, 86))):
         plan = tuning.lookup(bt, n, nblk, na)
         assert plan is not None

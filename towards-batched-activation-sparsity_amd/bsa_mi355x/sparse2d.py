@@ -56,7 +56,7 @@ def plan_2d(bt: int, n_dim: int, nn: int, nblk: int, na: int, device: torch.devi
     down_proj B=16 and B=64 with 16-64 of 64 output blocks."""
     explicit = plan is not None and any(plan.as_tuple())
     pl = resolve_plan(bt, n_dim, nblk, na, device, plan, dense=dense)
-    if pl.kind in (5, 6):
+    if pl.kind in (5, 6, 7):
         # variable-width column groups have no 2-D instantiation: the 16-column list-splitting
         # tile of the same rows instead
         if explicit:

@@ -1283,33 +1283,15 @@ __device__ __forceinline__ void vt_columns(int t, int G, int T, int* first, int*
 // KH = 1 (kind 6): no channel-half split; each of the WB waves loads both halves of every
 // weight subtile and activation row tile of its blocks (the two halves of an activation row are
 // one 128-byte line, requested back to back by one wave).
-// XL (kind 7, with KH = 1): the activations go through LDS instead of registers.  Each block's
-// BTT*16 rows x 64 channels arrive by 16-byte-per-lane loads straight into the wave's own slot
-// of LDS, 16 rows x 64 contiguous bytes per load (a quad of lanes covers one half row, where the
-// register form requests 16 rows x 16 bytes per quad), and are read back in MFMA order.  The
-// quad's 16-byte chunks are rotated by row / 4 so that those reads hit 16 distinct bank groups
-// per 16 lanes.  The registers the activations no longer hold leave room for four block-slice
-// waves; the wave reduction reuses each wave's own slots.
-template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SEL = false, bool XL = false>
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, int KH = 2, bool SEL = false>
 __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p) {
   constexpr int NW = KH * WB;
   constexpr int NT = 64 * NW;
   constexpr int F = BTT * NSUB;
   constexpr int HP = 3 - KH;  // halves per wave
-  static_assert(!XL || (KH == 1 && F <= DEPTH * BTT * HP), "kind 7: one wave per block, reduction in its slots");
-  constexpr int XS = XL ? NW * DEPTH * BTT * HP : 1;  // 1 KiB activation slots (kind 7)
-  constexpr int RS = XL ? 1 : NW * F;                  // 1 KiB reduction slots (kinds 5, 6)
   __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
-  __shared__ __attribute__((aligned(16))) u32x4 s_x[XS][64];
-  __shared__ __attribute__((aligned(16))) f32x4 s_red_own[RS][64];
+  __shared__ __attribute__((aligned(16))) f32x4 s_red[NW][F][64];
   __shared__ int s_misc[NW + 2];
-  // fragment f of wave ww's partial accumulators
-  auto s_red = [&](int ww, int f) -> f32x4* {
-    if constexpr (XL)
-      return (f32x4*)&s_x[ww * DEPTH * BTT * HP + f][0];
-    else
-      return &s_red_own[ww * F + f][0];
-  };
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1330,36 +1312,29 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
   const int cnt = pend - pbeg;
 
   const int blk_bytes = p.npad * 128;
-  // register activations (kinds 5, 6): lane = row (lane % 16) x 16-byte chunk (lane / 16)
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
   int xrow_off[BTT];
   bool xrow_ok[BTT];
-  // LDS activations (kind 7): lane 4q + c loads row q, chunk (c + q / 4) % 4 of a half, and
-  // MFMA lane m reads its (row m % 16, chunk m / 16) back at rd_pos
-  const int xq = XL ? lane >> 2 : lane & 15;
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi) {
-    const int row = y0 + 16 * bi + xq;
+    const int row = y0 + 16 * bi + (lane & 15);
     xrow_ok[bi] = row < p.bt;
     xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
   }
-  const int xcol = XL ? 8 * (((lane & 3) + (xq >> 2)) & 3) : 32 * h + 8 * (lane >> 4);
-  const int rd_pos = 4 * (lane & 15) + (((lane >> 4) - ((lane & 15) >> 2)) & 3);
+  const int xcol = 32 * h + 8 * (lane >> 4);
   int woff[NSUB];
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) woff[s] = s < nv ? lane * 16 + (st + s) * 2048 + h * 1024 : kOOB;
 
-  constexpr int XR = XL ? 1 : DEPTH;  // slots of register activations
   u32x4 wv[DEPTH][NSUB][HP];
-  u32x4 xv[XR][BTT][HP];
+  u32x4 xv[DEPTH][BTT][HP];
   f32x4 acc[BTT][NSUB];
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Slot d's loads for list entry t: kind 7 issues its activation loads (into LDS slot d)
-  // before the weights, so that the weights' waits cover them too.
-  auto issue = [&](int d, int t) {
+  auto issue = [&](u32x4 (&wd)[NSUB][HP], u32x4 (&xd)[BTT][HP], int t) {
     const bool in = (unsigned)t < (unsigned)cnt;
     const int q = in ? pbeg + t : 0;
     int blk = s_ids[q];
@@ -1367,63 +1342,31 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     const bool ok = in && blk >= 0 && blk < p.nblk;
     const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int hh = 0; hh < HP; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
     // A skipped slot reads zeros through an empty resource (as its weights do), so the lanes'
     // selects below do not depend on `ok`: a uniform branch there let the register allocator
     // reuse an in-flight load's register and drain the pipeline (vmcnt(0)) every block.
     const __amdgpu_buffer_rsrc_t xb = make_rsrc(p.x, ok ? p.x_bytes : 0);
     const int col = (ok ? blk : 0) * 64 + xcol;
-    if constexpr (XL) {
 #pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
+    for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-        for (int hh = 0; hh < HP; ++hh) {
-          const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
-          ld16_lds(xb, &s_x[((w * DEPTH + d) * BTT + bi) * HP + hh][0], v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh) wv[d][s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
-    if constexpr (!XL) {
-#pragma unroll
-      for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-        for (int hh = 0; hh < HP; ++hh) {
-          const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
-          xv[d][bi][hh] = ld16(xb, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
-        }
-    }
+      for (int hh = 0; hh < HP; ++hh) {
+        const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
+        xd[bi][hh] = ld16(xb, v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+      }
   };
 
-  auto compute = [&](int d) {
-    if constexpr (XL) {
-      u32x4 xl[BTT][HP];
+  auto compute = [&](const u32x4 (&wd)[NSUB][HP], const u32x4 (&xd)[BTT][HP]) {
+#pragma unroll
+    for (int hh = 0; hh < HP; ++hh)
 #pragma unroll
       for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-        for (int hh = 0; hh < HP; ++hh) xl[bi][hh] = s_x[((w * DEPTH + d) * BTT + bi) * HP + hh][rd_pos];
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh)
-#pragma unroll
-        for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xl[bi][hh], acc[bi][s]);
-    } else {
-#pragma unroll
-      for (int hh = 0; hh < HP; ++hh)
-#pragma unroll
-        for (int bi = 0; bi < BTT; ++bi)
-#pragma unroll
-          for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wv[d][s][hh], xv[d][bi][hh], acc[bi][s]);
-    }
-  };
-
-  // Kind 7: before slot d's LDS reads, every load up to its weights is done; `later` slots' loads
-  // (one slot = BTT*HP activation + NSUB*HP weight loads) and its own weights may be in flight.
-  constexpr int LX = BTT * HP, LW = NSUB * HP;
-  auto wait_slot = [&](auto later) {
-    if constexpr (XL) vmem_wait<LW + decltype(later)::value * (LX + LW)>();
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][hh], xd[bi][hh], acc[bi][s]);
   };
 
   // Rolling pipeline as in kind 1: leading out-of-range slots, branch-free passes, a drain.
@@ -1431,41 +1374,199 @@ __global__ __launch_bounds__(64 * KH * WB) void bsg_gemm_vt_kernel(GemmParams p)
     const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
     const int U = cnt + pad;
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(d, d - pad);
+    for (int d = 0; d < DEPTH; ++d) issue(wv[d], xv[d], d - pad);
     int u0 = 0;
     for (; u0 + DEPTH < U; u0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
-        wait_slot(std::integral_constant<int, DEPTH - 1>{});
-        compute(d);
+        compute(wv[d], xv[d]);
         BSG_TL_IF(2, u0 + d == pad);
-        issue(d, u0 + d + DEPTH - pad);
+        issue(wv[d], xv[d], u0 + d + DEPTH - pad);
         // Keep slot d's loads between its MFMAs and slot d+1's: left free, the scheduler may
         // gather a pass's MFMAs above its loads (each pass then waits for every block in
         // flight: vmcnt(0)), and which kernels it does this to changes with unrelated code.
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(wv[d], xv[d]);
+      BSG_TL_IF(2, u0 + d == pad);
+    }
+  }
+  BSG_TL_LOOP_END();
+
+  // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read: s_red is separate).
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) s_red[w][bi * NSUB + s][lane] = acc[bi][s];
+  __syncthreads();
+  for (int f = w; f < F; f += NW) {
+    f32x4 v = s_red[0][f][lane];
+#pragma unroll
+    for (int ww = 1; ww < NW; ++ww) v += s_red[ww][f][lane];
+    if (f % NSUB < nv) store_y<T, NSUB>(p, y0, st * 16, f, v);
+  }
+  BSG_TL(4);
+  BSG_TL_END(p, true);
+}
+
+// Kind 7 ("vtx"): the groups, waves and pipeline of kind 6, with each block's activations
+// loaded into the wave's own LDS slot instead of into registers: BTT*16 rows x 64 channels
+// arrive by 16-byte-per-lane loads, 16 rows x 64 contiguous bytes per load (a quad of lanes
+// covers one half row, where kind 6 requests 16 rows x 16 bytes per quad), and are read back in
+// MFMA order.  The quad's 16-byte chunks are rotated per row so that those reads hit distinct
+// bank groups in every 8 and every 16 consecutive lanes.  The registers the activations no longer hold leave room
+// for four block-slice waves at 64 rows; the wave reduction reuses each wave's own slots.  A
+// separate kernel from kind 6 so that kind 6's generated code stays as it is (its schedules
+// change with unrelated code in the same function).
+template <typename T, int BTT, int NSUB, int WB, int DEPTH, bool SEL = false>
+__global__ __launch_bounds__(64 * WB) void bsg_gemm_vtx_kernel(GemmParams p) {
+  constexpr int NT = 64 * WB;
+  constexpr int F = BTT * NSUB;
+  constexpr int SLOT = BTT * 2;  // 1 KiB activation pieces per block: row tile x channel half
+  static_assert(F <= DEPTH * SLOT, "the wave reduction reuses the wave's own activation slots");
+  __shared__ __attribute__((aligned(16))) int s_ids[BSG_MAX_NBLK];
+  __shared__ __attribute__((aligned(16))) u32x4 s_x[WB * DEPTH * SLOT][64];
+  __shared__ int s_misc[WB + 2];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's block slice
+  int tile, sk;
+  tile_of_group(1, &tile, &sk);
+  int st, nv;
+  vt_columns(tile, p.n_tiles, p.npad >> 4, &st, &nv);
+  const int y0 = blockIdx.y * (16 * BTT);
+  BSG_TL_DECL
+  BSG_TL(0);
+
+  const int na = stage_block_list<NT, true, SEL, SEL && BTT == 1>(p, s_ids, s_misc);
+  BSG_TL(1);
+  const int pbeg = (int)(((int64_t)na * w) / WB);
+  const int pend = (int)(((int64_t)na * (w + 1)) / WB);
+  const int cnt = pend - pbeg;
+
+  const int blk_bytes = p.npad * 128;
+  // lane 4q + c loads row q, 16-byte chunk (c - f(q)) % 4 of a 32-channel half, and MFMA lane m
+  // reads its (row r = m % 16, chunk m / 16) back at 4r + (chunk + f(r)) % 4, with
+  // f(r) = r/2 + r/8: any 8 consecutive lanes then read 8 distinct 16-byte bank groups of 128
+  // bytes, and any 16 lanes 16 distinct groups of 256 bytes
+  const int xq = lane >> 2;
+  auto rot = [](int r) { return ((r >> 1) + (r >> 3)) & 3; };
+  int xrow_off[BTT];
+  bool xrow_ok[BTT];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi) {
+    const int row = y0 + 16 * bi + xq;
+    xrow_ok[bi] = row < p.bt;
+    xrow_off[bi] = xrow_ok[bi] ? row * (int)p.ldx * 2 : 0;
+  }
+  const int xcol = 8 * (((lane & 3) - rot(xq)) & 3);
+  const int rd_pos = 4 * (lane & 15) + (((lane >> 4) + rot(lane & 15)) & 3);
+  int woff[NSUB];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) woff[s] = s < nv ? lane * 16 + (st + s) * 2048 : kOOB;
+  auto slot = [&](int d, int bi, int hh) -> u32x4* { return &s_x[(w * DEPTH + d) * SLOT + bi * 2 + hh][0]; };
+
+  u32x4 wv[DEPTH][NSUB][2];
+  f32x4 acc[BTT][NSUB];
+#pragma unroll
+  for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) acc[bi][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Slot d's loads for list entry t: the activations (into LDS slot d) first, then the weights,
+  // so that a wait for the weights covers the activations too.  A skipped entry loads through
+  // empty resources: zeros for the weights, and zeros written to the slot.
+  auto issue = [&](u32x4 (&wd)[NSUB][2], int d, int t) {
+    const bool in = (unsigned)t < (unsigned)cnt;
+    const int q = in ? pbeg + t : 0;
+    int blk = s_ids[q];
+    blk = __builtin_amdgcn_readfirstlane(blk);
+    const bool ok = in && blk >= 0 && blk < p.nblk;
+    const char* wb = (const char*)p.wp + (size_t)(ok ? blk : 0) * (size_t)blk_bytes;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ok ? blk_bytes : 0);
+    const __amdgpu_buffer_rsrc_t xb = make_rsrc(p.x, ok ? p.x_bytes : 0);
+    const int col = (ok ? blk : 0) * 64 + xcol;
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
+        ld16_lds(xb, slot(d, bi, hh), v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
+      }
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
+  };
+
+  // Slot d's activations, read from LDS into registers once every load up to its weights is
+  // done (`later` slots' loads, SLOT activation + 2 NSUB weight loads each, and slot d's own
+  // weights may still be in flight).  Each read comes right after an explicit wait inside the
+  // loop body, so no read follows the loop's back edge, where the compiler's own wait for the
+  // LDS loads would be for all of them (vmcnt(0)).
+  constexpr int LX = SLOT, LW = NSUB * 2;
+  u32x4 xl[BTT][2];
+  auto read = [&](int d, auto later) {
+    vmem_wait<LW + decltype(later)::value * (LX + LW)>();
+#pragma unroll
+    for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) xl[bi][hh] = slot(d, bi, hh)[rd_pos];
+  };
+  auto compute = [&](const u32x4 (&wd)[NSUB][2]) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int bi = 0; bi < BTT; ++bi)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) acc[bi][s] = Elem<T>::mfma(wd[s][hh], xl[bi][hh], acc[bi][s]);
+  };
+
+  // Rolling pipeline as in kind 1 (leading out-of-range slots, branch-free passes, a drain), with
+  // slot d+1's activations read before slot d's refill is waited on: compute slot d, refill it,
+  // read slot d+1.
+  if (cnt > 0) {
+    const int pad = (DEPTH - cnt % DEPTH) % DEPTH;
+    const int U = cnt + pad;
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(wv[d], d, d - pad);
+    read(0, std::integral_constant<int, DEPTH - 1>{});
+    int u0 = 0;
+    for (; u0 + DEPTH < U; u0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        compute(wv[d]);
+        BSG_TL_IF(2, u0 + d == pad);
+        issue(wv[d], d, u0 + d + DEPTH - pad);
+        // as in kinds 1 and 5/6: keep slot d's loads between its MFMAs and slot d+1's
+        __builtin_amdgcn_sched_barrier(0);
+        read((d + 1) % DEPTH, std::integral_constant<int, DEPTH - 1>{});
+      }
+    }
     static_for<DEPTH>([&](auto dd) {
       constexpr int d = decltype(dd)::value;
-      wait_slot(std::integral_constant<int, DEPTH - 1 - d>{});
-      compute(d);
+      compute(wv[d]);
       BSG_TL_IF(2, u0 + d == pad);
+      if constexpr (d + 1 < DEPTH) read(d + 1, std::integral_constant<int, DEPTH - 2 - d>{});
     });
   }
   BSG_TL_LOOP_END();
 
-  // The 2*WB accumulator sets meet in LDS (the list buffer is no longer read; kind 7 writes its
-  // own slots, whose activation loads have all been waited for and read).
+  // The WB accumulator sets meet in LDS, each wave writing into its own slots (every load into
+  // them has been waited for and read).
+  auto red = [&](int ww, int f) -> f32x4* { return (f32x4*)&s_x[ww * DEPTH * SLOT + f][0]; };
 #pragma unroll
   for (int bi = 0; bi < BTT; ++bi)
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) s_red(w, bi * NSUB + s)[lane] = acc[bi][s];
+    for (int s = 0; s < NSUB; ++s) red(w, bi * NSUB + s)[lane] = acc[bi][s];
   __syncthreads();
-  for (int f = w; f < F; f += NW) {
-    f32x4 v = s_red(0, f)[lane];
+  for (int f = w; f < F; f += WB) {
+    f32x4 v = red(0, f)[lane];
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) v += s_red(ww, f)[lane];
+    for (int ww = 1; ww < WB; ++ww) v += red(ww, f)[lane];
     if (f % NSUB < nv) store_y<T, NSUB>(p, y0, st * 16, f, v);
   }
   BSG_TL(4);
@@ -1504,7 +1605,7 @@ constexpr GemmFn kernel_sel() {
   } else if constexpr (KIND == KIND_VT1) {
     return bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, true>;
   } else {
-    return bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, true, true>;
+    return bsg_gemm_vtx_kernel<_Float16, B, S, W, D, true>;
   }
 }
 
@@ -1527,8 +1628,8 @@ constexpr GemmFn kernel_sel() {
   {KIND_VT1, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1>, bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1>, \
    nullptr, nullptr, kernel_sel<KIND_VT1, B, S, W, D>()}
 #define BSG_V1X(B, S, W, D)                                                                                    \
-  {KIND_VT1X, 16 * B, S, W, D, bsg_gemm_vt_kernel<_Float16, B, S, W, D, 1, false, true>,                        \
-   bsg_gemm_vt_kernel<__bf16, B, S, W, D, 1, false, true>, nullptr, nullptr, kernel_sel<KIND_VT1X, B, S, W, D>()}
+  {KIND_VT1X, 16 * B, S, W, D, bsg_gemm_vtx_kernel<_Float16, B, S, W, D>, bsg_gemm_vtx_kernel<__bf16, B, S, W, D>, \
+   nullptr, nullptr, kernel_sel<KIND_VT1X, B, S, W, D>()}
 #define BSG_F(R, S, W, D)                                                                                 \
   {KIND_FMA, R, S, W, D, bsg_gemm_fma_kernel<_Float16, R, S, W, D, false>, bsg_gemm_fma_kernel<__bf16, R, S, W, D, false>, \
    kernel_2d<KIND_FMA, _Float16, R, S, W, D>(), kernel_2d<KIND_FMA, __bf16, R, S, W, D>(), nullptr}
