@@ -647,10 +647,9 @@ def run_matrix(args, dev):
     if not args.only and focus != "down_b16_s500" and any(p.name == "down_b16_s500" for p in points):
         # the CPU-reference configuration beside it
         roofline["cpu_reference_point"] = roofline_of("down_b16_s500", True)
-    big = max((p for p in points if p.in_step and not p.dense), key=lambda p: (p.active_bytes, p.name), default=None)
-    if not args.only and big is not None and big.name != focus:
-        # the matrix's largest sparse launch (configs[3]'s GEMM), whichever kernel runs it
-        roofline["largest_sparse_point"] = roofline_of(big.name, True)
+    if not args.only and focus != "gate_up_b64_s520" and any(p.name == "gate_up_b64_s520" for p in points):
+        # configs[3]'s GEMM (gate/up B=64, 31 of 64 blocks), whichever kernel runs it
+        roofline["configs3_gemm_point"] = roofline_of("gate_up_b64_s520", True)
     if not args.only:
         # hipBLASLt (torch.mm, the reference's dense baseline) beside every dense point, so the
         # dense kernel the speedups divide by is shown against the vendor library at each batch

@@ -204,7 +204,7 @@ def test_bench_traffic_profile_per_roofline_point():
 def test_bench_roofline_profiles_match_the_tuned_kernel():
     """The committed traffic and counter summaries of the llama roofline points (the dominant
     kernel's largest sparse launch, gate/up B=16 s=0.638 with the shipped plans; the CPU-reference
-    point, down B=16 s=0.5; the matrix's largest sparse launch, gate/up B=64 s=0.52) were taken on
+    point, down B=16 s=0.5; configs[3]'s GEMM, gate/up B=64 s=0.52) were taken on
     the kernel their tuned plans launch now (a retune that changes the kernel makes them stale)."""
     bench = _bench_module()
     from bsa_mi355x import tuning
