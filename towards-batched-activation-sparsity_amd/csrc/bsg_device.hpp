@@ -1496,10 +1496,14 @@ __global__ __launch_bounds__(64 * WB) void bsg_gemm_vtx_kernel(GemmParams p) {
         const bool v = xrow_ok[bi] && col + 32 * hh < p.K;
         ld16_lds(xb, slot(d, bi, hh), v ? xrow_off[bi] + (col + 32 * hh) * 2 : kOOB);
       }
+    // The waits by count (read below) rely on this order: every activation load of the slot
+    // before its weight loads, and the slot's loads before the next slot's.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) wd[s][hh] = ld16_stream(wr, woff[s] + hh * 1024);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Slot d's activations, read from LDS into registers once every load up to its weights is
