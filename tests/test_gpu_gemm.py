@@ -308,6 +308,36 @@ def test_device_count(dev):
     assert_close(out.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, idx[:17]), "device count")
 
 
+@pytest.mark.parametrize("plan", [(1, 16, 4, 4, 16, 1), (3, 16, 2, 4, 16, 1), (2, 16, 4, 4, 16, 2),
+                                  (1, 16, 4, 4, 16, 4), (1, 48, 4, 4, 16, 5), (1, 48, 4, 4, 16, 6),
+                                  (1, 32, 4, 4, 16, 7), (1, 32, 4, 2, 32, 7)])
+def test_device_count_every_kind(dev, plan):
+    """The device-side count in every MFMA kernel kind: counts below, at and above the list's
+    capacity (clamped to it) and negative (no block: zeros), each launch on the same plan and
+    workspace, against the oracle on the entries that count."""
+    bt, k, n, cap = 16, 4096, 1000, 40
+    x, w_nk, _ = case(16, bt, k, n, 1, "normal")
+    rng = np.random.default_rng(4)
+    idx = rng.permutation(64)[:cap].astype(np.int32)
+    xt, it = to_dev(x, dev), to_dev(idx, dev)
+    packed = bsa.pack_weight(to_dev(w_nk, dev))
+    p = bsa.Plan(*plan)
+    for d in (17, cap, 55, 0, -3, 1):
+        out = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        cnt = torch.tensor([d], dtype=torch.int32, device=dev)
+        print(f"device count plan={plan} count={d}", flush=True)
+        used = bsa.gemm_packed(xt, packed, n, it, out, plan=p, num_active=cap, num_active_dev=cnt,
+                               workspace_prefix="devcnt")
+        assert used.as_tuple() == p.as_tuple(), used
+        torch.cuda.synchronize()
+        keep = idx[:max(0, min(d, cap))]
+        y = out.float().cpu().numpy()
+        if keep.size == 0:
+            assert np.count_nonzero(y) == 0, (plan, d)
+        else:
+            assert_close(y, orc.gemm_ref64(x, w_nk, keep), f"plan {plan} count {d}")
+
+
 def test_pack_layout_bit_exact(dev):
     """Device packing == oracle tile_permute(pack_kmajor(W)) bit for bit (both layouts)."""
     for n, k in ((100, 1000), (4096, 256), (48, 64)):
