@@ -647,13 +647,16 @@ def test_variable_width_column_groups(dev, bt, k, n, na):
         bsa.gemm_packed(xt, packed, n, it, again, plan=p, workspace_prefix="vt")
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), again.view(torch.int16))
-    p = bsa.Plan(1, 48, 4, 4, rows, 5)
-    dense = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
-    bsa.gemm_packed(xt, packed, n, None, dense, plan=p, workspace_prefix="vt")
+    # dense and bitmap modes (the list built on the device) in each kind
     bm = torch.zeros(orc.nblk_of(k), dtype=torch.uint8, device=dev)
     bm[it.long()] = 1
-    bout = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
-    bsa.gemm_packed(xt, packed, n, None, bout, bitmap=bm, plan=p, workspace_prefix="vt")
-    torch.cuda.synchronize()
-    assert_close(dense.float().cpu().numpy(), orc.gemm_ref64(x, w_nk, np.arange(orc.nblk_of(k))), "kind 5 dense")
-    assert_close(bout.float().cpu().numpy(), ref, "kind 5 bitmap")
+    ref_dense = orc.gemm_ref64(x, w_nk, np.arange(orc.nblk_of(k)))
+    for kind, cols, waves, depth in ((5, 48, 4, 4), (6, 48, 2, 4), (7, 32, 4, 4 if rows == 16 else 2)):
+        p = bsa.Plan(1, cols, waves, depth, rows, kind)
+        dense = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        bsa.gemm_packed(xt, packed, n, None, dense, plan=p, workspace_prefix="vt")
+        bout = torch.full((bt, n), float("nan"), dtype=F16, device=dev)
+        bsa.gemm_packed(xt, packed, n, None, bout, bitmap=bm, plan=p, workspace_prefix="vt")
+        torch.cuda.synchronize()
+        assert_close(dense.float().cpu().numpy(), ref_dense, f"kind {kind} dense")
+        assert_close(bout.float().cpu().numpy(), ref, f"kind {kind} bitmap")
