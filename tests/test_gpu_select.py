@@ -103,6 +103,11 @@ def _fused(dev, x, w_nk, k, plan=None):
     (64, 4096, 11008, 31, (1, 48, 2, 4, 64, 6)),  # variable-width groups, waves split blocks
     (16, 4096, 12288, 23, (1, 48, 4, 4, 16, 5)),  # variable-width groups, channel-half waves
     (64, 4096, 22016, 31, (1, 96, 2, 4, 64, 5)),  # 5-6 subtiles per group
+    (64, 4096, 11008, 31, (1, 48, 4, 2, 64, 7)),  # activations through LDS
+    (64, 4096, 12288, 31, (1, 48, 8, 2, 64, 7)),  # eight block-slice waves
+    (64, 11008, 4096, 83, (1, 32, 4, 2, 32, 7)),  # 172 blocks, two 32-row groups
+    (16, 4096, 4096, 23, (1, 32, 4, 4, 16, 7)),
+    (2, 4096, 4096, 13, (1, 32, 4, 4, 16, 7)),    # the work-groups score the blocks themselves
 ])
 def test_fused_select_gemm_every_kind(dev, bt, kdim, n, k, plan):
     """Selection + GEMM for every kernel kind and edge k, with the top-k either ranked inside
