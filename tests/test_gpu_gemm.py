@@ -564,12 +564,22 @@ def test_in_kernel_sort_at_its_limit_and_past_it(dev):
                  "1500 sorted by a sort launch")
 
 
-@pytest.mark.parametrize("plan", [(1, 16, 2, 4, 16, 1), (3, 16, 4, 4, 32, 2), (2, 16, 8, 4, 64, 4), (1, 16, 4, 4, 4, 3)])
-def test_strided_rows_and_side_stream(dev, plan):
+@pytest.mark.parametrize("k,plan", [
+    (4096, (1, 16, 2, 4, 16, 1)), (4096, (3, 16, 4, 4, 32, 2)), (4096, (2, 16, 8, 4, 64, 4)),
+    (4096, (1, 16, 4, 4, 4, 3)), (4096, (1, 48, 4, 4, 16, 5)), (4096, (1, 48, 2, 4, 64, 6)),
+    (4096, (1, 48, 4, 2, 64, 7)), (4096, (1, 32, 8, 2, 32, 7)),
+    # K not a multiple of 64: the last block holds 40 or 8 channels, the rest of it is NaN padding
+    (1000, (1, 16, 2, 4, 16, 1)), (1000, (1, 48, 4, 4, 16, 5)), (1000, (1, 48, 2, 4, 64, 6)),
+    (1000, (1, 48, 4, 2, 64, 7)), (1032, (1, 32, 4, 4, 16, 7)), (1032, (2, 16, 4, 4, 32, 2)),
+])
+def test_strided_rows_and_side_stream(dev, k, plan):
     """X and Y as row-strided views (ldx > K, ldy > N), launched on a side stream: the padding
     columns of X hold NaN (any read past K would poison Y) and those of Y keep a sentinel."""
-    bt, k, n, na = 40, 4096, 1000, 25
+    bt, n = 40, 1000
+    na = min(25, orc.nblk_of(k))
     x, w_nk, idx = case(19, bt, k, n, na)
+    if k % 64 and orc.nblk_of(k) - 1 not in idx:
+        idx = np.sort(np.append(idx[1:], orc.nblk_of(k) - 1)).astype(np.int32)  # the partial block counts
     x_wide = torch.full((bt, k + 64), float("nan"), dtype=F16, device=dev)
     x_wide[:, :k] = to_dev(x, dev)
     y_wide = torch.full((bt, n + 24), 7.0, dtype=F16, device=dev)
@@ -582,7 +592,7 @@ def test_strided_rows_and_side_stream(dev, plan):
     s.synchronize()
     y = y_wide.float().cpu().numpy()
     assert np.all(y[:, n:] == 7.0), "columns past N were written"
-    assert_close(y[:, :n], orc.gemm_ref64(x, w_nk, idx), f"strided {plan}")
+    assert_close(y[:, :n], orc.gemm_ref64(x, w_nk, idx), f"strided K={k} {plan}")
 
 
 @pytest.mark.parametrize("bt,plan", [
